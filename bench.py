@@ -1,0 +1,236 @@
+"""Throughput of the gfx950 MHSEA kernels on BASELINE.json's synthetic configurations.
+
+Default (the driver's run): configuration c2 — fused forward + JVP, float32,
+q/k/v [B=1024, N=64, H=8, D=32], one tangent per input, 36 physical sites of 64, seed 1.
+One "step" is one fwd+JVP of the whole batch (one kernel launch, inputs resident in HBM).
+
+Prints ONE JSON line with walkers/s, the roofline of the dominant kernel (live HIP-event
+timing on the launch stream) and a CPU baseline (the jnp path's torch-CPU port, timed on
+a bounded walker sample on this host; see oracle/cpu_baseline.py).
+
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--config c1..c5]
+                       [--cpu-budget SECONDS] [--no-cpu-baseline]
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+if ROOT not in sys.path:
+    sys.path.insert(0, ROOT)
+
+METRIC = "fwd+JVP attention walkers/sec at B=1024,L=64; % of MFMA/HBM roofline"
+HBM_PEAK_GBS = 8000.0
+FP32_PEAK_TFLOPS = 157.3
+BF16_PEAK_TFLOPS = 2516.6
+
+# name: (work, B, N, H, D, n_phys, T, dtype, seed, description)
+CONFIGS = {
+    "c1": ("fwd", 256, 8, 4, 32, 8, 0, "f32", 0, "attention forward, fp32, [256,8,4,32], no padding"),
+    "c2": ("fwd_jvp", 1024, 64, 8, 32, 36, 1, "f32", 1,
+           "forward + JVP, fp32, [1024,64,8,32], 36/64 physical sites (6x6 lattice)"),
+    "c3": ("fwd_vjp", 4096, 64, 8, 64, 48, 0, "bf16", 2,
+           "forward + VJP, bf16 I/O fp32 accumulate, [4096,64,8,64], 48/64 physical sites"),
+    "c4": ("fwd_jvp", 512, 256, 8, 64, 225, 1, "f32", 3,
+           "large-N forward + JVP, fp32, [512,256,8,64], 225/256 physical sites (15x15)"),
+    "c5": ("fwd_jvp", 128, 1024, 16, 64, 1000, 2, "bf16", 4,
+           "large-N stress forward + 2 JVP directions, bf16 I/O, [128,1024,16,64], 1000/1024 sites"),
+}
+
+
+def algorithmic(work, B, N, H, D, n_phys, T, esize):
+    """Algorithmic bytes and flops of one step.
+
+    padded: every [B,N,H,D] tensor read or written once at the padded shape, plus the mask
+            (uint8); flops (2 + 4T) G for fwd+JVP, 2G fwd, 6G fwd+VJP, G = 2 N^2 D per
+            (walker, head), recompute not counted.
+    effective: the same with the mask taken into account — inputs are needed only on
+            physical rows (a masked row never influences a result), outputs are written on
+            every row (zeros included), and only physical x physical pairs carry flops.
+    """
+    rowb = H * D * esize  # bytes of one site row of one [B,N,H,D] tensor
+    if work == "fwd":
+        n_in, n_out, g_mult, lse_b = 3, 1, 2, 0
+    elif work == "fwd_jvp":
+        n_in, n_out, g_mult, lse_b = 3 + 3 * T, 1 + T, 2 + 4 * T, 0
+    elif work == "fwd_vjp":
+        # fwd: q,k,v in, out + lse out; bwd: q,k,v,out,dout + lse in, dq,dk,dv out
+        n_in, n_out, g_mult, lse_b = 3 + 5, 1 + 3, 6, 2 * N * H * 4
+    else:
+        raise ValueError(work)
+    padded_bytes = B * (N * rowb * (n_in + n_out) + N + lse_b)
+    eff_bytes = B * (n_phys * rowb * n_in + N * rowb * n_out + N + lse_b)
+    padded_flops = B * H * g_mult * 2 * N * N * D
+    eff_flops = B * H * g_mult * 2 * n_phys * n_phys * D
+    return dict(padded_bytes=padded_bytes, eff_bytes=eff_bytes, padded_flops=padded_flops,
+                eff_flops=eff_flops)
+
+
+def roofline(bytes_, flops, t_s, dtype):
+    peak_c = BF16_PEAK_TFLOPS if dtype == "bf16" else FP32_PEAK_TFLOPS
+    t_hbm = bytes_ / (HBM_PEAK_GBS * 1e9)
+    t_cmp = flops / (peak_c * 1e12)
+    if t_hbm >= t_cmp:
+        ach = bytes_ / t_s / 1e9
+        return {"bound": "hbm", "achieved": ach, "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": ach / HBM_PEAK_GBS}
+    ach = flops / t_s / 1e12
+    return {"bound": "mfma", "achieved": ach, "peak": peak_c, "unit": "TFLOP/s", "frac": ach / peak_c}
+
+
+def traffic_from_profile(config):
+    """HBM bytes per launch measured by rocprofv3 --pmc (FETCH_SIZE, WRITE_SIZE), scaled by
+    the copy-kernel calibration, if a summary for this configuration is committed."""
+    path = os.path.join(ROOT, "profiles", f"traffic_{config}.json")
+    if not os.path.exists(path):
+        return None
+    with open(path) as fh:
+        rec = json.load(fh)
+    return rec.get("traffic_bytes_per_launch")
+
+
+def main(argv=None):
+    ap = argparse.ArgumentParser(description=__doc__.splitlines()[0])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--config", default="c2", choices=sorted(CONFIGS))
+    ap.add_argument("--cpu-budget", type=float, default=15.0)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    args = ap.parse_args(argv)
+
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU only (this build has no multi-GPU path); got --gpus {args.gpus}",
+              file=sys.stderr)
+        return 2
+
+    import torch
+
+    from hamiltonzero_amd import _native
+
+    lib = _native.lib()
+    work, B, N, H, D, n_phys, T, dtype, seed, desc = CONFIGS[args.config]
+    tdt = torch.bfloat16 if dtype == "bf16" else torch.float32
+    hz_dtype = _native.HZ_DTYPE_BF16 if dtype == "bf16" else _native.HZ_DTYPE_F32
+    esize = 2 if dtype == "bf16" else 4
+    dev = torch.device("cuda:0")
+
+    # Synthetic inputs: default_rng(seed); draw order q, k, v, tangents (per direction
+    # qt, kt, vt), cotangent; q/k/v scaled by 1/sqrt(D).
+    rng = np.random.default_rng(seed)
+    shape = (B, N, H, D)
+
+    def draw(scale):
+        x = rng.standard_normal(shape, dtype=np.float32)
+        if scale != 1.0:
+            x *= np.float32(scale)
+        return torch.from_numpy(x).to(device=dev, dtype=tdt)
+
+    q, k, v = draw(D ** -0.5), draw(D ** -0.5), draw(D ** -0.5)
+    tans = []
+    for _ in range(T):
+        tans.append([draw(1.0), draw(1.0), draw(1.0)])
+    dout = draw(1.0) if work == "fwd_vjp" else None
+    mask = torch.zeros((B, N), dtype=torch.uint8, device=dev)
+    mask[:, :n_phys] = 1
+    stream = torch.cuda.current_stream(dev)
+    s = stream.cuda_stream
+    out = torch.empty(shape, dtype=tdt, device=dev)
+    P = lambda t: None if t is None else t.data_ptr()  # noqa: E731
+
+    if work == "fwd":
+        def step():
+            _native.check(lib.hz_mhsea_fwd(s, P(q), P(k), None, P(v), P(mask), P(out), None,
+                                           B, N, H, D, hz_dtype, 1.0, 0))
+    elif work == "fwd_jvp":
+        qt = torch.stack([t[0] for t in tans]).contiguous()
+        kt = torch.stack([t[1] for t in tans]).contiguous()
+        vt = torch.stack([t[2] for t in tans]).contiguous()
+        del tans
+        tout = torch.empty((T, *shape), dtype=tdt, device=dev)
+
+        def step():
+            _native.check(lib.hz_mhsea_fwd_jvp(s, P(q), P(k), None, P(v), P(mask), P(qt), P(kt), None, P(vt), T,
+                                               P(out), None, P(tout), B, N, H, D, hz_dtype, 1.0, 0))
+    else:
+        lse = torch.empty((B, N, H), dtype=torch.float32, device=dev)
+        dq, dk, dv = (torch.empty(shape, dtype=tdt, device=dev) for _ in range(3))
+
+        def step():
+            _native.check(lib.hz_mhsea_fwd(s, P(q), P(k), None, P(v), P(mask), P(out), P(lse),
+                                           B, N, H, D, hz_dtype, 1.0, 0))
+            _native.check(lib.hz_mhsea_bwd(s, P(q), P(k), None, P(v), P(mask), P(lse), P(out), P(dout),
+                                           P(dq), P(dk), None, P(dv), B, N, H, D, hz_dtype, 1.0, 0))
+
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    ev0 = torch.cuda.Event(enable_timing=True)
+    ev1 = torch.cuda.Event(enable_timing=True)
+    ev0.record(stream)
+    for _ in range(args.steps):
+        step()
+    ev1.record(stream)
+    torch.cuda.synchronize()
+    ms = ev0.elapsed_time(ev1) / args.steps
+    t_s = ms / 1e3
+    walkers_s = B / t_s
+
+    alg = algorithmic(work, B, N, H, D, n_phys, T, esize)
+    roof = roofline(alg["eff_bytes"], alg["eff_flops"], t_s, dtype)
+    roof["traffic"] = traffic_from_profile(args.config)
+    roof["basis"] = "mask-aware algorithmic bytes/flops (physical rows in, all rows out)"
+    roof["bytes_per_step"] = alg["eff_bytes"]
+    roof["flops_per_step"] = alg["eff_flops"]
+    roof_padded = roofline(alg["padded_bytes"], alg["padded_flops"], t_s, dtype)
+    roof_padded["bytes_per_step"] = alg["padded_bytes"]
+    roof_padded["flops_per_step"] = alg["padded_flops"]
+
+    cpu = None
+    if not args.no_cpu_baseline:
+        from oracle import cpu_baseline
+
+        threads = int(os.environ.get("OMP_NUM_THREADS", os.cpu_count() or 1))
+        sample = {"c1": 256, "c2": 64, "c3": 32, "c4": 4, "c5": 1}[args.config]
+        r = cpu_baseline.time_walkers_per_s(work, sample, N, H, D, n_phys, seed, T=max(T, 1),
+                                            bf16_inputs=(dtype == "bf16"), budget_s=args.cpu_budget,
+                                            threads=threads)
+        cpu = {
+            "value": r["walkers_per_s"],
+            "unit": "walkers/s",
+            "cores": r["threads"],
+            "kind": "port",
+            "sample": f"{sample} walkers of the same shape/mask/seed recipe, {r['reps']} reps in "
+                      f"{r['seconds']:.1f} s, torch-CPU fp32 jnp-path port ({r['cpu_model']})",
+        }
+
+    line = {
+        "metric": METRIC,
+        "value": walkers_s,
+        "unit": "walkers/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": ms,
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16" if dtype == "bf16" else "f32",
+        "data": "synthetic (numpy default_rng, N(0,1)/sqrt(D) q/k/v, N(0,1) tangents)",
+        "config": {"workload": f"{args.config}: {desc}", "B": B, "N": N, "H": H, "D": D,
+                   "n_phys": n_phys, "T": T, "work": work},
+        "roofline": roof,
+        "roofline_padded": roof_padded,
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(line), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

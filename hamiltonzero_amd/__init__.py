@@ -1,0 +1,32 @@
+"""MI355X (gfx950) implementation of HamiltonZero's MHSEA attention hot path.
+
+Public surface, named after the reference modules it replaces:
+
+* :mod:`hamiltonzero_amd.edge_attention` — ``mhsea_tuned_edge_attention`` and
+  ``reference_edge_attention`` (``src/hamiltonzero/model/pallas_attention.py``).
+* :mod:`hamiltonzero_amd.mhsea_tuned` — ``mhsea_with_tuned_ad`` and the primitive pair
+  (``src/hamiltonzero/model/_pallas_attn/mhsea_tuned.py``).
+* :mod:`hamiltonzero_amd.kernels` — tensor-level calls of the C ABI
+  (``include/hz_mhsea.h``): forward, tangent, fused forward+tangent, backward.
+"""
+
+from .edge_attention import mhsea_tuned_edge_attention, reference_edge_attention
+from .mhsea_tuned import (
+    mhsea_ad,
+    mhsea_tuned_ad,
+    mhsea_tuned_ad_lin,
+    mhsea_tuned_ad_lin_transpose,
+    mhsea_tuned_jvp,
+    mhsea_with_tuned_ad,
+)
+
+__all__ = [
+    "mhsea_ad",
+    "mhsea_tuned_ad",
+    "mhsea_tuned_ad_lin",
+    "mhsea_tuned_ad_lin_transpose",
+    "mhsea_tuned_edge_attention",
+    "mhsea_tuned_jvp",
+    "mhsea_with_tuned_ad",
+    "reference_edge_attention",
+]

@@ -1,0 +1,109 @@
+"""ctypes binding of ``libhz_mhsea.so`` (the C ABI declared in ``include/hz_mhsea.h``).
+
+The library is the only compute path of this package: there is no CPU fallback. A
+missing library raises :class:`NativeLibraryMissing` on first use.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import threading
+from pathlib import Path
+
+LIB_PATH = Path(__file__).resolve().parent / "_lib" / "libhz_mhsea.so"
+
+HZ_DTYPE_F32 = 0
+HZ_DTYPE_BF16 = 1
+HZ_FLAG_KEY_MASK = 1
+HZ_FLAG_E_QKH = 2
+HZ_MAX_N = 16384
+
+HZ_OK = 0
+HZ_EINVAL = 1
+HZ_ENULL = 2
+HZ_EALIGN = 3
+HZ_ELAUNCH = 4
+
+# Every symbol include/hz_mhsea.h declares.
+EXPORTED_SYMBOLS = (
+    "hz_version",
+    "hz_last_error",
+    "hz_mhsea_fwd",
+    "hz_mhsea_jvp",
+    "hz_mhsea_fwd_jvp",
+    "hz_mhsea_bwd",
+)
+
+
+class NativeLibraryMissing(RuntimeError):
+    """libhz_mhsea.so has not been built (run ``python -m hamiltonzero_amd.build``)."""
+
+
+class HzError(RuntimeError):
+    """A non-zero status from the C ABI; ``code`` is the HZ_E* value."""
+
+    def __init__(self, code: int, message: str):
+        super().__init__(f"hz_mhsea error {code}: {message}")
+        self.code = code
+
+
+_lock = threading.Lock()
+_lib: ctypes.CDLL | None = None
+
+_P = ctypes.c_void_p
+_I64 = ctypes.c_int64
+_INT = ctypes.c_int
+_F = ctypes.c_float
+
+_SIGNATURES = {
+    "hz_version": ([], _INT),
+    "hz_last_error": ([], ctypes.c_char_p),
+    # stream, q, k, e, v, mask, out, lse, B, N, H, D, dtype, scale, flags
+    "hz_mhsea_fwd": ([_P, _P, _P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _INT, _F, _INT], _INT),
+    # stream, q, k, e, v, mask, out, lse, qt, kt, et, vt, T, tout, B, N, H, D, dtype, scale, flags
+    "hz_mhsea_jvp": (
+        [_P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _I64, _P, _I64, _I64, _I64, _I64, _INT, _F, _INT],
+        _INT,
+    ),
+    # stream, q, k, e, v, mask, qt, kt, et, vt, T, out, lse, tout, B, N, H, D, dtype, scale, flags
+    "hz_mhsea_fwd_jvp": (
+        [_P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _I64, _P, _P, _P, _I64, _I64, _I64, _I64, _INT, _F, _INT],
+        _INT,
+    ),
+    # stream, q, k, e, v, mask, lse, out, dout, dq, dk, de, dv, B, N, H, D, dtype, scale, flags
+    "hz_mhsea_bwd": (
+        [_P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _INT, _F, _INT],
+        _INT,
+    ),
+}
+
+
+def lib() -> ctypes.CDLL:
+    """Load (once) and return the native library, with argument types declared."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    with _lock:
+        if _lib is None:
+            if not LIB_PATH.exists():
+                raise NativeLibraryMissing(
+                    f"{LIB_PATH} is missing: build it with `python -m hamiltonzero_amd.build`"
+                )
+            handle = ctypes.CDLL(str(LIB_PATH))
+            for name, (argtypes, restype) in _SIGNATURES.items():
+                fn = getattr(handle, name)
+                fn.argtypes = argtypes
+                fn.restype = restype
+            _lib = handle
+    return _lib
+
+
+def check(status: int) -> None:
+    """Raise :class:`HzError` for a non-zero status, with the library's message."""
+    if status != HZ_OK:
+        msg = lib().hz_last_error()
+        raise HzError(status, msg.decode() if msg else "")
+
+
+def version() -> int:
+    return int(lib().hz_version())

@@ -1,0 +1,250 @@
+// C ABI of the MHSEA kernels: argument validation, error reporting and dispatch.
+// Every check runs on the host before anything is enqueued, so an invalid call never
+// reaches the GPU.
+#include <cmath>
+#include <cstdarg>
+#include <cstdio>
+
+#include "../../include/hz_mhsea.h"
+#include "mhsea_launch.h"
+
+namespace {
+
+thread_local char g_err[512] = "";
+
+int fail(int code, const char* fmt, ...) {
+  va_list ap;
+  va_start(ap, fmt);
+  std::vsnprintf(g_err, sizeof(g_err), fmt, ap);
+  va_end(ap);
+  return code;
+}
+
+int ok() {
+  g_err[0] = '\0';
+  return HZ_OK;
+}
+
+bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+// Shared validation of the dimensions and flags (mirrors the shape assertions of
+// _validate_primals, mhsea_tuned.py:29-50, and the head-dim set of pallas_attention.py:13).
+int check_dims(int64_t B, int64_t N, int64_t H, int64_t D, int dtype, int flags) {
+  if (B < 1 || H < 1) return fail(HZ_EINVAL, "B and H must be >= 1, got B=%lld H=%lld", (long long)B, (long long)H);
+  if (N < 1 || N > HZ_MAX_N)
+    return fail(HZ_EINVAL, "N must be in [1, %d], got %lld", HZ_MAX_N, (long long)N);
+  if (D != 8 && D != 16 && D != 32 && D != 64)
+    return fail(HZ_EINVAL, "head dimension must be one of [8, 16, 32, 64], got %lld", (long long)D);
+  if (dtype != HZ_DTYPE_F32 && dtype != HZ_DTYPE_BF16)
+    return fail(HZ_EINVAL, "dtype must be HZ_DTYPE_F32 (0) or HZ_DTYPE_BF16 (1), got %d", dtype);
+  if (flags & ~(HZ_FLAG_KEY_MASK | HZ_FLAG_E_QKH)) return fail(HZ_EINVAL, "unknown flag bits 0x%x", flags);
+  const int64_t nwg = B * H * ((N + 63) / 64);
+  if (nwg > 0x7fffffffLL) return fail(HZ_EINVAL, "B*H*ceil(N/64) = %lld exceeds the grid limit", (long long)nwg);
+  if (B * N * H * N > (int64_t(1) << 46))
+    return fail(HZ_EINVAL, "B*N*H*N = %lld exceeds the supported tensor size", (long long)(B * N * H * N));
+  return HZ_OK;
+}
+
+#define HZ_REQUIRE(ptr)                                                     \
+  do {                                                                      \
+    if ((ptr) == nullptr) return fail(HZ_ENULL, "%s must not be NULL", #ptr); \
+    if (!aligned16(ptr)) return fail(HZ_EALIGN, "%s must be 16-byte aligned", #ptr); \
+  } while (0)
+
+#define HZ_OPTIONAL(ptr)                                                    \
+  do {                                                                      \
+    if ((ptr) != nullptr && !aligned16(ptr))                                \
+      return fail(HZ_EALIGN, "%s must be 16-byte aligned", #ptr);           \
+  } while (0)
+
+void set_e_strides(int64_t N, int64_t H, int flags, int64_t& sq, int64_t& sh, int64_t& sk) {
+  if (flags & HZ_FLAG_E_QKH) {  // [B, Nq, Nk, H]
+    sq = N * H;
+    sk = H;
+    sh = 1;
+  } else {  // [B, Nq, H, Nk]
+    sq = H * N;
+    sh = N;
+    sk = 1;
+  }
+}
+
+size_t elem_bytes(int dtype) { return dtype == HZ_DTYPE_BF16 ? 2 : 4; }
+
+int launched(hipError_t err) {
+  if (err != hipSuccess) return fail(HZ_ELAUNCH, "kernel launch failed: %s", hipGetErrorString(err));
+  return ok();
+}
+
+hz::FwdParams fwd_params(const void* q, const void* k, const void* e, const void* v,
+                         const uint8_t* mask, int64_t B, int64_t N, int64_t H, int64_t D,
+                         float scale, int flags) {
+  hz::FwdParams p{};
+  p.q = q;
+  p.k = k;
+  p.v = v;
+  p.e = e;
+  p.mask = mask;
+  p.B = static_cast<int>(B);
+  p.N = static_cast<int>(N);
+  p.H = static_cast<int>(H);
+  p.t_stride = B * N * H * D;
+  p.et_stride = B * N * H * N;
+  set_e_strides(N, H, flags, p.e_sq, p.e_sh, p.e_sk);
+  p.scale = scale;
+  p.key_mask = (flags & HZ_FLAG_KEY_MASK) ? 1 : 0;
+  p.masked_lse = -10000.0f + std::log(static_cast<float>(N));
+  return p;
+}
+
+// Runs the forward / tangent family over all T directions in groups of at most two
+// (the kernels are specialised for T in {0, 1, 2}); the primal is written by the first
+// group only.
+int run_tangent_groups(hz::FwdParams p, int64_t D, int64_t T, bool given_lse, int dtype,
+                       hipStream_t stream, void* tout, const void* qt, const void* kt,
+                       const void* et, const void* vt) {
+  const size_t eb = elem_bytes(dtype);
+  const int64_t ts = p.t_stride, es = p.et_stride;
+  void* const out0 = p.out;
+  float* const lse0 = p.lse;
+  for (int64_t t0 = 0; t0 < T; t0 += 2) {
+    const int tn = static_cast<int>(T - t0 < 2 ? T - t0 : 2);
+    auto shift = [&](const void* base, int64_t stride) -> const void* {
+      return base == nullptr ? nullptr : static_cast<const char*>(base) + t0 * stride * eb;
+    };
+    p.qt = shift(qt, ts);
+    p.kt = shift(kt, ts);
+    p.vt = shift(vt, ts);
+    p.et = shift(et, es);
+    p.tout = static_cast<char*>(tout) + t0 * ts * eb;
+    if (!given_lse && t0 > 0) {
+      // Later groups rewrite identical primal values; point them at the same buffers so
+      // the call never needs scratch memory.
+      p.out = out0;
+      p.lse = lse0;
+    }
+    hipError_t err = hz::launch_fwd(p, static_cast<int>(D), tn, given_lse, dtype, stream);
+    if (err != hipSuccess) return launched(err);
+  }
+  return ok();
+}
+
+}  // namespace
+
+extern "C" {
+
+int hz_version(void) { return HZ_MHSEA_VERSION; }
+
+const char* hz_last_error(void) { return g_err; }
+
+int hz_mhsea_fwd(hipStream_t stream, const void* q, const void* k, const void* e,
+                 const void* v, const uint8_t* mask, void* out, float* lse, int64_t B,
+                 int64_t N, int64_t H, int64_t D, int dtype, float scale, int flags) {
+  if (int rc = check_dims(B, N, H, D, dtype, flags)) return rc;
+  HZ_REQUIRE(q);
+  HZ_REQUIRE(k);
+  HZ_REQUIRE(v);
+  if (mask == nullptr) return fail(HZ_ENULL, "mask must not be NULL");
+  HZ_REQUIRE(out);
+  HZ_OPTIONAL(e);
+  HZ_OPTIONAL(lse);
+  if (!std::isfinite(scale)) return fail(HZ_EINVAL, "scale must be finite");
+  hz::FwdParams p = fwd_params(q, k, e, v, mask, B, N, H, D, scale, flags);
+  p.out = out;
+  p.lse = lse;
+  return launched(hz::launch_fwd(p, static_cast<int>(D), 0, false, dtype, stream));
+}
+
+int hz_mhsea_jvp(hipStream_t stream, const void* q, const void* k, const void* e,
+                 const void* v, const uint8_t* mask, const void* out, const float* lse,
+                 const void* qt, const void* kt, const void* et, const void* vt, int64_t T,
+                 void* tout, int64_t B, int64_t N, int64_t H, int64_t D, int dtype,
+                 float scale, int flags) {
+  if (int rc = check_dims(B, N, H, D, dtype, flags)) return rc;
+  if (T < 1 || T > 4096) return fail(HZ_EINVAL, "T must be in [1, 4096], got %lld", (long long)T);
+  HZ_REQUIRE(q);
+  HZ_REQUIRE(k);
+  HZ_REQUIRE(v);
+  if (mask == nullptr) return fail(HZ_ENULL, "mask must not be NULL");
+  HZ_REQUIRE(out);
+  HZ_REQUIRE(lse);
+  HZ_REQUIRE(tout);
+  HZ_OPTIONAL(e);
+  HZ_OPTIONAL(qt);
+  HZ_OPTIONAL(kt);
+  HZ_OPTIONAL(et);
+  HZ_OPTIONAL(vt);
+  if (!std::isfinite(scale)) return fail(HZ_EINVAL, "scale must be finite");
+  hz::FwdParams p = fwd_params(q, k, e, v, mask, B, N, H, D, scale, flags);
+  p.out_in = out;
+  p.lse_in = lse;
+  return run_tangent_groups(p, D, T, true, dtype, stream, tout, qt, kt, et, vt);
+}
+
+int hz_mhsea_fwd_jvp(hipStream_t stream, const void* q, const void* k, const void* e,
+                     const void* v, const uint8_t* mask, const void* qt, const void* kt,
+                     const void* et, const void* vt, int64_t T, void* out, float* lse,
+                     void* tout, int64_t B, int64_t N, int64_t H, int64_t D, int dtype,
+                     float scale, int flags) {
+  if (int rc = check_dims(B, N, H, D, dtype, flags)) return rc;
+  if (T < 1 || T > 4096) return fail(HZ_EINVAL, "T must be in [1, 4096], got %lld", (long long)T);
+  HZ_REQUIRE(q);
+  HZ_REQUIRE(k);
+  HZ_REQUIRE(v);
+  if (mask == nullptr) return fail(HZ_ENULL, "mask must not be NULL");
+  HZ_REQUIRE(out);
+  HZ_REQUIRE(tout);
+  HZ_OPTIONAL(e);
+  HZ_OPTIONAL(lse);
+  HZ_OPTIONAL(qt);
+  HZ_OPTIONAL(kt);
+  HZ_OPTIONAL(et);
+  HZ_OPTIONAL(vt);
+  if (!std::isfinite(scale)) return fail(HZ_EINVAL, "scale must be finite");
+  hz::FwdParams p = fwd_params(q, k, e, v, mask, B, N, H, D, scale, flags);
+  p.out = out;
+  p.lse = lse;
+  return run_tangent_groups(p, D, T, false, dtype, stream, tout, qt, kt, et, vt);
+}
+
+int hz_mhsea_bwd(hipStream_t stream, const void* q, const void* k, const void* e,
+                 const void* v, const uint8_t* mask, const float* lse, const void* out,
+                 const void* dout, void* dq, void* dk, void* de, void* dv, int64_t B,
+                 int64_t N, int64_t H, int64_t D, int dtype, float scale, int flags) {
+  if (int rc = check_dims(B, N, H, D, dtype, flags)) return rc;
+  HZ_REQUIRE(q);
+  HZ_REQUIRE(k);
+  HZ_REQUIRE(v);
+  if (mask == nullptr) return fail(HZ_ENULL, "mask must not be NULL");
+  HZ_REQUIRE(lse);
+  HZ_REQUIRE(out);
+  HZ_REQUIRE(dout);
+  HZ_REQUIRE(dq);
+  HZ_REQUIRE(dk);
+  HZ_REQUIRE(dv);
+  HZ_OPTIONAL(e);
+  HZ_OPTIONAL(de);
+  if (!std::isfinite(scale)) return fail(HZ_EINVAL, "scale must be finite");
+  hz::BwdParams p{};
+  p.q = q;
+  p.k = k;
+  p.v = v;
+  p.e = e;
+  p.mask = mask;
+  p.lse = lse;
+  p.out = out;
+  p.dout = dout;
+  p.dq = dq;
+  p.dk = dk;
+  p.dv = dv;
+  p.de = de;
+  p.B = static_cast<int>(B);
+  p.N = static_cast<int>(N);
+  p.H = static_cast<int>(H);
+  set_e_strides(N, H, flags, p.e_sq, p.e_sh, p.e_sk);
+  p.scale = scale;
+  p.key_mask = (flags & HZ_FLAG_KEY_MASK) ? 1 : 0;
+  return launched(hz::launch_bwd(p, static_cast<int>(D), dtype, stream));
+}
+
+}  // extern "C"

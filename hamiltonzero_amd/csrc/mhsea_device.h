@@ -1,0 +1,171 @@
+// Device-side helpers shared by the MHSEA kernels (gfx950 / CDNA4, wave64).
+//
+// Matrix-core convention used throughout (v_mfma_f32_16x16x4_f32, one 16x16 block):
+//   lane l = 16*g + c   (g = l / 16 in 0..3, c = l % 16)
+//   A operand (16 x 4):  lane supplies A[row = c][k = g]
+//   B operand (4 x 16):  lane supplies B[k = g][col = c]
+//   C/D       (16 x 16): lane holds    C[row = 4*g + r][col = c], r = 0..3 (a v4f)
+// The contraction index k may be any permutation of the summed dimension as long as the
+// A and B operands of one instruction agree, which the kernels use to keep every lane's
+// operands contiguous in memory.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace hz {
+
+typedef float v4f __attribute__((ext_vector_type(4)));
+
+constexpr float kLog2e = 1.4426950408889634f;
+constexpr float kLn2 = 0.6931471805599453f;
+// Score of an invalid (query, key) pair under the square mask (utils.py:51-52).
+constexpr float kMaskScore = -10000.0f;
+
+__device__ __forceinline__ v4f mfma16x4(float a, float b, v4f c) {
+  return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
+}
+
+__device__ __forceinline__ v4f zero4() { return v4f{0.f, 0.f, 0.f, 0.f}; }
+
+// bfloat16 <-> float32. Round-to-nearest-even on the way down; NaN stays NaN.
+__device__ __forceinline__ float bf16_to_f32(uint16_t x) {
+  return __uint_as_float(static_cast<uint32_t>(x) << 16);
+}
+__device__ __forceinline__ uint16_t f32_to_bf16(float f) {
+  uint32_t u = __float_as_uint(f);
+  if ((u & 0x7fffffffu) > 0x7f800000u) return static_cast<uint16_t>((u >> 16) | 0x40u);
+  u += 0x7fffu + ((u >> 16) & 1u);
+  return static_cast<uint16_t>(u >> 16);
+}
+
+// Storage policy: F32 tensors are float, BF16 tensors are uint16_t bit patterns.
+struct F32 {
+  typedef float T;
+  static constexpr int kBytes = 4;
+};
+struct BF16 {
+  typedef uint16_t T;
+  static constexpr int kBytes = 2;
+};
+
+// Load 4 consecutive elements (16 B aligned for F32, 8 B for BF16) as float.
+template <class S>
+__device__ __forceinline__ float4 load4(const void* base, int64_t off);
+template <>
+__device__ __forceinline__ float4 load4<F32>(const void* base, int64_t off) {
+  return *reinterpret_cast<const float4*>(static_cast<const float*>(base) + off);
+}
+template <>
+__device__ __forceinline__ float4 load4<BF16>(const void* base, int64_t off) {
+  uint2 u = *reinterpret_cast<const uint2*>(static_cast<const uint16_t*>(base) + off);
+  return make_float4(__uint_as_float(u.x << 16), __uint_as_float(u.x & 0xffff0000u),
+                     __uint_as_float(u.y << 16), __uint_as_float(u.y & 0xffff0000u));
+}
+
+// Load 2 consecutive elements (8 B aligned for F32, 4 B for BF16) as float.
+template <class S>
+__device__ __forceinline__ float2 load2(const void* base, int64_t off);
+template <>
+__device__ __forceinline__ float2 load2<F32>(const void* base, int64_t off) {
+  return *reinterpret_cast<const float2*>(static_cast<const float*>(base) + off);
+}
+template <>
+__device__ __forceinline__ float2 load2<BF16>(const void* base, int64_t off) {
+  uint32_t u = *reinterpret_cast<const uint32_t*>(static_cast<const uint16_t*>(base) + off);
+  return make_float2(__uint_as_float(u << 16), __uint_as_float(u & 0xffff0000u));
+}
+
+template <class S>
+__device__ __forceinline__ float load1(const void* base, int64_t off);
+template <>
+__device__ __forceinline__ float load1<F32>(const void* base, int64_t off) {
+  return static_cast<const float*>(base)[off];
+}
+template <>
+__device__ __forceinline__ float load1<BF16>(const void* base, int64_t off) {
+  return bf16_to_f32(static_cast<const uint16_t*>(base)[off]);
+}
+
+template <class S>
+__device__ __forceinline__ void store4(void* base, int64_t off, float a, float b, float c,
+                                       float d);
+template <>
+__device__ __forceinline__ void store4<F32>(void* base, int64_t off, float a, float b,
+                                            float c, float d) {
+  *reinterpret_cast<float4*>(static_cast<float*>(base) + off) = make_float4(a, b, c, d);
+}
+template <>
+__device__ __forceinline__ void store4<BF16>(void* base, int64_t off, float a, float b,
+                                             float c, float d) {
+  uint2 u;
+  u.x = static_cast<uint32_t>(f32_to_bf16(a)) | (static_cast<uint32_t>(f32_to_bf16(b)) << 16);
+  u.y = static_cast<uint32_t>(f32_to_bf16(c)) | (static_cast<uint32_t>(f32_to_bf16(d)) << 16);
+  *reinterpret_cast<uint2*>(static_cast<uint16_t*>(base) + off) = u;
+}
+
+template <class S>
+__device__ __forceinline__ void store1(void* base, int64_t off, float a);
+template <>
+__device__ __forceinline__ void store1<F32>(void* base, int64_t off, float a) {
+  static_cast<float*>(base)[off] = a;
+}
+template <>
+__device__ __forceinline__ void store1<BF16>(void* base, int64_t off, float a) {
+  static_cast<uint16_t*>(base)[off] = f32_to_bf16(a);
+}
+
+// Sum / max over the four lane groups g that share one column c (lanes c, c+16, c+32, c+48).
+__device__ __forceinline__ float group_sum(float x) {
+  x += __shfl_xor(x, 16, 64);
+  x += __shfl_xor(x, 32, 64);
+  return x;
+}
+__device__ __forceinline__ float group_max(float x) {
+  x = fmaxf(x, __shfl_xor(x, 16, 64));
+  x = fmaxf(x, __shfl_xor(x, 32, 64));
+  return x;
+}
+
+// Offset of element (b, n, h, d) of a [B, N, H, D] tensor.
+__device__ __forceinline__ int64_t bnhd(int b, int n, int h, int N, int H, int D) {
+  return ((static_cast<int64_t>(b) * N + n) * H + h) * D;
+}
+
+// Per-walker compaction of the mask into the list of physical sites (ascending).
+// Writes idx[0..count) and returns count to every thread of the workgroup.
+// Must be called by all threads of a 256-thread workgroup; `scratch` holds 5 ints.
+__device__ __forceinline__ int compact_mask(const uint8_t* __restrict__ mask_row, int N,
+                                            int16_t* __restrict__ idx,
+                                            int* __restrict__ scratch) {
+  const int tid = threadIdx.x;
+  const int wave = tid >> 6;
+  const int lane = tid & 63;
+  int total = 0;
+  for (int base = 0; base < N; base += 256) {
+    const int pos = base + tid;
+    const bool on = (pos < N) && (mask_row[pos] != 0);
+    const uint64_t bal = __ballot(on);
+    if (lane == 0) scratch[wave] = __popcll(bal);
+    __syncthreads();
+    int before = total;
+    for (int w = 0; w < wave; ++w) before += scratch[w];
+    const int mine = __popcll(bal & ((uint64_t(1) << lane) - 1));
+    if (on) idx[before + mine] = static_cast<int16_t>(pos);
+    total += scratch[0] + scratch[1] + scratch[2] + scratch[3];
+    __syncthreads();
+  }
+  return total;
+}
+
+// Map blockIdx.x to a logical workgroup id so that consecutive logical ids (which share
+// K/V rows of one walker and head) land on the same XCD. Workgroups are dispatched to
+// the 8 XCDs round-robin by hardware id.
+__device__ __forceinline__ int64_t xcd_logical_block(int64_t hw, int64_t nblocks) {
+  constexpr int kXcd = 8;
+  if (nblocks % kXcd != 0) return hw;
+  const int64_t per = nblocks / kXcd;
+  return (hw % kXcd) * per + hw / kXcd;
+}
+
+}  // namespace hz

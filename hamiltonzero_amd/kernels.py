@@ -1,0 +1,251 @@
+"""Torch-tensor entry points of the gfx950 MHSEA kernels.
+
+Thin, allocation-owning wrappers over the C ABI (``include/hz_mhsea.h``): they check
+shapes, dtypes and devices, allocate outputs with torch on the inputs' device and
+enqueue the kernels on torch's current stream. No computation happens here; the HIP
+library is required.
+
+Layouts follow the reference primitives (``_pallas_attn/utils.py:21-36``):
+``q, k, v: [B, N, H, D]``, ``e: [B, N, H, N]`` (or ``[B, N, N, H]`` with
+``e_layout="qkh"``), ``mask: [B, N]`` bool, ``lse: [B, N, H]`` float32, tangents
+``[T, B, N, H, D]`` or a single ``[B, N, H, D]`` direction.
+"""
+
+from __future__ import annotations
+
+from typing import Optional, Tuple
+
+import torch
+
+from . import _native
+
+Tensor = torch.Tensor
+
+_DTYPES = {torch.float32: _native.HZ_DTYPE_F32, torch.bfloat16: _native.HZ_DTYPE_BF16}
+SUPPORTED_HEAD_DIMS = (8, 16, 32, 64)
+
+
+def _ptr(t: Optional[Tensor]) -> Optional[int]:
+    return None if t is None else t.data_ptr()
+
+
+def _stream(device: torch.device) -> int:
+    return torch.cuda.current_stream(device).cuda_stream
+
+
+def _flags(key_mask: bool, e_layout: str) -> int:
+    if e_layout not in ("qhk", "qkh"):
+        raise ValueError(f"e_layout must be 'qhk' or 'qkh', got {e_layout!r}")
+    return (_native.HZ_FLAG_KEY_MASK if key_mask else 0) | (
+        _native.HZ_FLAG_E_QKH if e_layout == "qkh" else 0
+    )
+
+
+def _check_primals(q: Tensor, k: Tensor, v: Tensor, mask: Tensor, e: Optional[Tensor], e_layout: str):
+    if q.dim() != 4:
+        raise ValueError(f"q must have rank 4 [B, N, H, D], got shape {tuple(q.shape)}")
+    B, N, H, D = q.shape
+    if q.dtype not in _DTYPES:
+        raise TypeError(f"q.dtype must be float32 or bfloat16, got {q.dtype}")
+    if not q.is_cuda:
+        raise ValueError("MHSEA kernels need GPU tensors (q is on %s)" % q.device)
+    if D not in SUPPORTED_HEAD_DIMS:
+        raise ValueError(f"head dimension must be one of {list(SUPPORTED_HEAD_DIMS)}, got {D}")
+    for name, t in (("k", k), ("v", v)):
+        if tuple(t.shape) != (B, N, H, D):
+            raise ValueError(f"{name}.shape must be {(B, N, H, D)}, got {tuple(t.shape)}")
+        if t.dtype != q.dtype:
+            raise TypeError(f"{name}.dtype must equal q.dtype ({q.dtype}), got {t.dtype}")
+        if t.device != q.device:
+            raise ValueError(f"{name} is on {t.device}, q on {q.device}")
+    if tuple(mask.shape) != (B, N):
+        raise ValueError(f"mask.shape must be {(B, N)}, got {tuple(mask.shape)}")
+    if e is not None:
+        want = (B, N, H, N) if e_layout == "qhk" else (B, N, N, H)
+        if tuple(e.shape) != want:
+            raise ValueError(f"e.shape must be {want}, got {tuple(e.shape)}")
+        if e.dtype != q.dtype:
+            raise TypeError(f"e.dtype must equal q.dtype ({q.dtype}), got {e.dtype}")
+    return B, N, H, D
+
+
+def _c(t: Optional[Tensor]) -> Optional[Tensor]:
+    return None if t is None else t.contiguous()
+
+
+def _mask_u8(mask: Tensor, device: torch.device) -> Tensor:
+    m = mask.to(device=device)
+    if m.dtype == torch.bool:
+        return m.contiguous().view(torch.uint8)
+    return (m != 0).contiguous().view(torch.uint8)
+
+
+def _tangent(t: Optional[Tensor], shape: tuple, dtype, name: str) -> Tuple[Optional[Tensor], int]:
+    """Normalise one tangent operand to [T, *shape]; returns (tensor or None, T or 0)."""
+    if t is None:
+        return None, 0
+    if tuple(t.shape) == shape:
+        t = t.unsqueeze(0)
+    if t.dim() != len(shape) + 1 or tuple(t.shape[1:]) != shape:
+        raise ValueError(f"{name}.shape must be {shape} or [T, *{shape}], got {tuple(t.shape)}")
+    if t.dtype != dtype:
+        raise TypeError(f"{name}.dtype must be {dtype}, got {t.dtype}")
+    return t.contiguous(), t.shape[0]
+
+
+def _tangents(q, e_shape, qt, kt, et, vt):
+    shape = tuple(q.shape)
+    qt, tq = _tangent(qt, shape, q.dtype, "qt")
+    kt, tk = _tangent(kt, shape, q.dtype, "kt")
+    vt, tv = _tangent(vt, shape, q.dtype, "vt")
+    et, te = _tangent(et, e_shape, q.dtype, "et")
+    counts = {x for x in (tq, tk, tv, te) if x}
+    if len(counts) > 1:
+        raise ValueError(f"tangent directions disagree: {sorted(counts)}")
+    T = counts.pop() if counts else 1
+    return qt, kt, et, vt, T
+
+
+def mhsea_fwd(
+    q: Tensor,
+    k: Tensor,
+    v: Tensor,
+    mask: Tensor,
+    e: Optional[Tensor] = None,
+    *,
+    scale: float = 1.0,
+    key_mask: bool = False,
+    e_layout: str = "qhk",
+    with_lse: bool = True,
+) -> Tuple[Tensor, Optional[Tensor]]:
+    """Forward: returns ``(out, lse)`` (lse is None when ``with_lse`` is False)."""
+    B, N, H, D = _check_primals(q, k, v, mask, e, e_layout)
+    q, k, v, e = _c(q), _c(k), _c(v), _c(e)
+    m = _mask_u8(mask, q.device)
+    out = torch.empty_like(q)
+    lse = torch.empty((B, N, H), dtype=torch.float32, device=q.device) if with_lse else None
+    _native.check(
+        _native.lib().hz_mhsea_fwd(
+            _stream(q.device), _ptr(q), _ptr(k), _ptr(e), _ptr(v), _ptr(m), _ptr(out), _ptr(lse),
+            B, N, H, D, _DTYPES[q.dtype], float(scale), _flags(key_mask, e_layout),
+        )
+    )
+    return out, lse
+
+
+def mhsea_jvp(
+    q: Tensor,
+    k: Tensor,
+    v: Tensor,
+    mask: Tensor,
+    out: Tensor,
+    lse: Tensor,
+    qt: Optional[Tensor] = None,
+    kt: Optional[Tensor] = None,
+    vt: Optional[Tensor] = None,
+    e: Optional[Tensor] = None,
+    et: Optional[Tensor] = None,
+    *,
+    scale: float = 1.0,
+    key_mask: bool = False,
+    e_layout: str = "qhk",
+) -> Tensor:
+    """Tangent of the forward given its primal ``(out, lse)`` (the reference's lin primitive).
+
+    Tangents are ``[B, N, H, D]`` (one direction) or ``[T, B, N, H, D]``; ``None`` is a
+    zero tangent. Returns ``tout`` shaped like the given tangents.
+    """
+    B, N, H, D = _check_primals(q, k, v, mask, e, e_layout)
+    e_shape = (B, N, H, N) if e_layout == "qhk" else (B, N, N, H)
+    batched = any(t is not None and t.dim() == 5 for t in (qt, kt, vt)) or (et is not None and et.dim() == 5)
+    qt, kt, et, vt, T = _tangents(q, e_shape, qt, kt, et, vt)
+    if tuple(out.shape) != (B, N, H, D) or out.dtype != q.dtype:
+        raise ValueError("out must match q in shape and dtype")
+    if tuple(lse.shape) != (B, N, H) or lse.dtype != torch.float32:
+        raise ValueError(f"lse must be float32 of shape {(B, N, H)}")
+    q, k, v, e, out, lse = _c(q), _c(k), _c(v), _c(e), _c(out), _c(lse)
+    m = _mask_u8(mask, q.device)
+    tout = torch.empty((T, B, N, H, D), dtype=q.dtype, device=q.device)
+    _native.check(
+        _native.lib().hz_mhsea_jvp(
+            _stream(q.device), _ptr(q), _ptr(k), _ptr(e), _ptr(v), _ptr(m), _ptr(out), _ptr(lse),
+            _ptr(qt), _ptr(kt), _ptr(et), _ptr(vt), T, _ptr(tout),
+            B, N, H, D, _DTYPES[q.dtype], float(scale), _flags(key_mask, e_layout),
+        )
+    )
+    return tout if batched else tout[0]
+
+
+def mhsea_fwd_jvp(
+    q: Tensor,
+    k: Tensor,
+    v: Tensor,
+    mask: Tensor,
+    qt: Optional[Tensor] = None,
+    kt: Optional[Tensor] = None,
+    vt: Optional[Tensor] = None,
+    e: Optional[Tensor] = None,
+    et: Optional[Tensor] = None,
+    *,
+    scale: float = 1.0,
+    key_mask: bool = False,
+    e_layout: str = "qhk",
+    with_lse: bool = True,
+) -> Tuple[Tensor, Optional[Tensor], Tensor]:
+    """Fused forward + tangents: returns ``(out, lse, tout)`` in one pass over K/V."""
+    B, N, H, D = _check_primals(q, k, v, mask, e, e_layout)
+    e_shape = (B, N, H, N) if e_layout == "qhk" else (B, N, N, H)
+    batched = any(t is not None and t.dim() == 5 for t in (qt, kt, vt)) or (et is not None and et.dim() == 5)
+    qt, kt, et, vt, T = _tangents(q, e_shape, qt, kt, et, vt)
+    q, k, v, e = _c(q), _c(k), _c(v), _c(e)
+    m = _mask_u8(mask, q.device)
+    out = torch.empty_like(q)
+    lse = torch.empty((B, N, H), dtype=torch.float32, device=q.device) if with_lse else None
+    tout = torch.empty((T, B, N, H, D), dtype=q.dtype, device=q.device)
+    _native.check(
+        _native.lib().hz_mhsea_fwd_jvp(
+            _stream(q.device), _ptr(q), _ptr(k), _ptr(e), _ptr(v), _ptr(m),
+            _ptr(qt), _ptr(kt), _ptr(et), _ptr(vt), T, _ptr(out), _ptr(lse), _ptr(tout),
+            B, N, H, D, _DTYPES[q.dtype], float(scale), _flags(key_mask, e_layout),
+        )
+    )
+    return out, lse, (tout if batched else tout[0])
+
+
+def mhsea_bwd(
+    q: Tensor,
+    k: Tensor,
+    v: Tensor,
+    mask: Tensor,
+    lse: Tensor,
+    out: Tensor,
+    dout: Tensor,
+    e: Optional[Tensor] = None,
+    *,
+    want_de: bool = True,
+    scale: float = 1.0,
+    key_mask: bool = False,
+    e_layout: str = "qhk",
+) -> Tuple[Tensor, Tensor, Optional[Tensor], Tensor]:
+    """Reverse mode: returns ``(dq, dk, de, dv)`` (de is None when not requested)."""
+    B, N, H, D = _check_primals(q, k, v, mask, e, e_layout)
+    for name, t in (("out", out), ("dout", dout)):
+        if tuple(t.shape) != (B, N, H, D) or t.dtype != q.dtype:
+            raise ValueError(f"{name} must match q in shape and dtype")
+    if tuple(lse.shape) != (B, N, H) or lse.dtype != torch.float32:
+        raise ValueError(f"lse must be float32 of shape {(B, N, H)}")
+    q, k, v, e, lse, out, dout = map(_c, (q, k, v, e, lse, out, dout))
+    m = _mask_u8(mask, q.device)
+    dq = torch.empty_like(q)
+    dk = torch.empty_like(q)
+    dv = torch.empty_like(q)
+    e_shape = (B, N, H, N) if e_layout == "qhk" else (B, N, N, H)
+    de = torch.empty(e_shape, dtype=q.dtype, device=q.device) if want_de else None
+    _native.check(
+        _native.lib().hz_mhsea_bwd(
+            _stream(q.device), _ptr(q), _ptr(k), _ptr(e), _ptr(v), _ptr(m), _ptr(lse), _ptr(out),
+            _ptr(dout), _ptr(dq), _ptr(dk), _ptr(de), _ptr(dv),
+            B, N, H, D, _DTYPES[q.dtype], float(scale), _flags(key_mask, e_layout),
+        )
+    )
+    return dq, dk, de, dv

@@ -1,0 +1,154 @@
+/*
+ * hz_mhsea.h — C ABI of the MI355X (gfx950) MHSEA attention kernels.
+ *
+ * MHSEA = masked, edge-biased multi-head self attention:
+ *     S   = scale * Q K^T + E            (per walker b, head h)
+ *     P   = softmax_k(S)                 restricted to valid (query, key) pairs
+ *     out = P V
+ * together with its forward-mode tangent (JVP) and reverse-mode cotangent (VJP).
+ *
+ * This header replaces the reference's Pallas primitives
+ *   mhsea_tuned_ad_p      (src/hamiltonzero/model/_pallas_attn/mhsea_tuned.py:72-174)
+ *   mhsea_tuned_ad_lin_p  (src/hamiltonzero/model/_pallas_attn/mhsea_tuned.py:175-240)
+ *   mhsea_full_ad_p / _lin_p (src/hamiltonzero/model/_pallas_attn/mhsea_full_ad.py:32-185)
+ * and the jnp op reference_edge_attention
+ *   (src/hamiltonzero/model/pallas_attention.py:22-37).
+ *
+ * Conventions shared by every entry point
+ * ---------------------------------------
+ *  - All tensor pointers are DEVICE pointers, row-major, C-contiguous.
+ *      q, k, v, out, dq, dk, dv, dout : [B, N, H, D]   ("sites-major", as the
+ *                                        reference BlockSpecs in _pallas_attn/utils.py:21-36)
+ *      tangents qt, kt, vt, tout       : [T, B, N, H, D]   (T tangent directions)
+ *      e, de                           : [B, N, H, N]  (query, head, key)  default, or
+ *                                        [B, N, N, H]  with HZ_FLAG_E_QKH (op-level layout,
+ *                                        pallas_attention.py:45, so no transpose pass)
+ *      et                              : [T, <layout of e>]
+ *      mask                            : [B, N] uint8 (0 = padded/virtual site, else physical)
+ *      lse                             : [B, N, H] float32 (natural log-sum-exp per query row)
+ *  - dtype: HZ_DTYPE_F32 (all float tensors float32) or HZ_DTYPE_BF16 (q, k, v, e, all
+ *    tangents/cotangents and float outputs are bfloat16; lse is always float32; every
+ *    reduction and the softmax run in float32).
+ *  - D must be 8, 16, 32 or 64 (the reference's supported head dims,
+ *    pallas_attention.py:13).  1 <= N <= HZ_MAX_N.  B, H >= 1.
+ *  - Optional pointers (documented per call) may be NULL: a NULL bias / bias tangent means
+ *    zero, a NULL tangent means a zero tangent (ad.instantiate_zeros, mhsea_tuned.py:107-110).
+ *  - scale multiplies Q K^T before the bias is added. The primitives take pre-scaled Q and
+ *    pass scale = 1 (mhsea.py:14-31); the op-level wrapper passes D^-1/2 (pallas_attention.py:31).
+ *  - Mask semantics (flags):
+ *      default ("square", the primitive, mhsea.py:18-25 + mhsea_tuned.py:91):
+ *          a (query i, key j) pair is valid iff mask[i] && mask[j]; scores of invalid
+ *          pairs are -1e4 (utils.py:51-52). Rows of masked queries are written as exact
+ *          zeros in out / tout / dq, and their lse is -1e4 + log(N).
+ *      HZ_FLAG_KEY_MASK (reference_edge_attention, pallas_attention.py:34-36):
+ *          only keys are masked (additive -1e9); every query row is computed. If no key
+ *          of a walker is physical, all keys are used (the exact-arithmetic limit of the
+ *          additive mask).
+ *  - Every call is enqueue-only on `stream` (no host synchronisation), allocates nothing,
+ *    fully overwrites its outputs (including masked rows), and is deterministic
+ *    (no atomics). Calls on distinct output buffers are re-entrant.
+ *  - Return value: 0 on success, otherwise an HZ_E* code; hz_last_error() then returns a
+ *    thread-local message. Argument errors are detected on the host before any GPU work.
+ */
+#ifndef HZ_MHSEA_H
+#define HZ_MHSEA_H
+
+#include <stdint.h>
+#include <hip/hip_runtime_api.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define HZ_MHSEA_VERSION 100 /* 1.0.0 */
+#define HZ_MAX_N 16384
+
+enum hz_dtype { HZ_DTYPE_F32 = 0, HZ_DTYPE_BF16 = 1 };
+
+enum hz_flags {
+  HZ_FLAG_KEY_MASK = 1, /* reference_edge_attention masking instead of the square mask */
+  HZ_FLAG_E_QKH = 2     /* e / et / de are [B, N(query), N(key), H] */
+};
+
+enum hz_status {
+  HZ_OK = 0,
+  HZ_EINVAL = 1,   /* bad dimension, dtype, flag or T */
+  HZ_ENULL = 2,    /* a required pointer is NULL */
+  HZ_EALIGN = 3,   /* a tensor pointer is not 16-byte aligned */
+  HZ_ELAUNCH = 4   /* the HIP runtime rejected a kernel launch */
+};
+
+/* Library version (HZ_MHSEA_VERSION). */
+int hz_version(void);
+
+/* Message for the last non-zero status returned on this thread ("" if none). */
+const char* hz_last_error(void);
+
+/*
+ * Forward. Replaces mhsea_tuned_ad_p's impl (_outer_impl, mhsea_tuned.py:76-92 ->
+ * mhsea_forward, custom_gradients.py:24-75 -> mhsea_kernel, mhsea.py:11-31).
+ * Writes out [B,N,H,D] and, if lse != NULL, lse [B,N,H].
+ * Optional: e (NULL = no bias), lse.
+ */
+int hz_mhsea_fwd(hipStream_t stream,
+                 const void* q, const void* k, const void* e, const void* v,
+                 const uint8_t* mask,
+                 void* out, float* lse,
+                 int64_t B, int64_t N, int64_t H, int64_t D,
+                 int dtype, float scale, int flags);
+
+/*
+ * Tangent of the forward given its primal outputs. Replaces mhsea_tuned_ad_lin_p's impl
+ * (_inner_impl, mhsea_tuned.py:179-198 -> mhsea_tangent_pallas,
+ * mhsea_tuned_jvp.py:104-222), with the same 11 operands in the same order plus a native
+ * tangent axis T (the reference instead broadcasts the primals T times,
+ * mhsea_tuned.py:144-148):
+ *     tout[t] = P(dS_t) V + P vt[t] - rowsum(P o dS_t) out,    P = exp(S - lse)
+ *     dS_t    = scale (qt[t] K^T + Q kt[t]^T) + et[t]           (valid pairs, else 0)
+ * Required: q, k, v, mask, out, lse, tout. Optional: e, qt, kt, et, vt. T >= 1.
+ */
+int hz_mhsea_jvp(hipStream_t stream,
+                 const void* q, const void* k, const void* e, const void* v,
+                 const uint8_t* mask, const void* out, const float* lse,
+                 const void* qt, const void* kt, const void* et, const void* vt,
+                 int64_t T, void* tout,
+                 int64_t B, int64_t N, int64_t H, int64_t D,
+                 int dtype, float scale, int flags);
+
+/*
+ * Fused forward + T tangents in one pass (P is formed once per tile and shared by all
+ * tangents). Same results as hz_mhsea_fwd followed by hz_mhsea_jvp, i.e. as the
+ * reference's _outer_jvp (mhsea_tuned.py:104-118), without the round trip of out/lse
+ * through HBM. Required: q, k, v, mask, out, tout. Optional: e, lse, qt, kt, et, vt.
+ */
+int hz_mhsea_fwd_jvp(hipStream_t stream,
+                     const void* q, const void* k, const void* e, const void* v,
+                     const uint8_t* mask,
+                     const void* qt, const void* kt, const void* et, const void* vt,
+                     int64_t T,
+                     void* out, float* lse, void* tout,
+                     int64_t B, int64_t N, int64_t H, int64_t D,
+                     int dtype, float scale, int flags);
+
+/*
+ * Reverse mode: cotangents of (q, k, e, v) for the upstream cotangent dout. Replaces the
+ * transpose rule _inner_transpose (mhsea_tuned.py:206-221 -> mhsea_backward,
+ * custom_gradients.py:78-228 -> mhsea_q_vjp_kernel :231-285, mhsea_kv_vjp_kernel
+ * :288-347):
+ *     dP = dout V^T,  delta = rowsum(out o dout),  dS = P o (dP - delta)  (valid pairs)
+ *     dq = scale dS K,  dk = scale dS^T Q,  dv = P^T dout,  de = dS
+ * Required: q, k, v, mask, lse, out, dout, dq, dk, dv. Optional: e, de (NULL = not
+ * requested). Rows of masked sites are exact zeros in dq, dk, dv and de.
+ */
+int hz_mhsea_bwd(hipStream_t stream,
+                 const void* q, const void* k, const void* e, const void* v,
+                 const uint8_t* mask, const float* lse, const void* out, const void* dout,
+                 void* dq, void* dk, void* de, void* dv,
+                 int64_t B, int64_t N, int64_t H, int64_t D,
+                 int dtype, float scale, int flags);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* HZ_MHSEA_H */

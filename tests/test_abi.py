@@ -1,0 +1,121 @@
+"""C-ABI checks that need no GPU: the library loads, exports every symbol the header
+declares, and rejects invalid arguments on the host before any GPU work."""
+
+import ctypes
+import re
+from pathlib import Path
+
+import pytest
+
+from hamiltonzero_amd import _native
+
+HEADER = Path(__file__).resolve().parents[1] / "include" / "hz_mhsea.h"
+
+
+def header_functions():
+    text = HEADER.read_text()
+    return sorted(set(re.findall(r"^\s*(?:int|const char\*)\s+(hz_\w+)\s*\(", text, flags=re.M)))
+
+
+@pytest.fixture(scope="module")
+def lib():
+    if not _native.LIB_PATH.exists():
+        pytest.skip("libhz_mhsea.so not built (run python -m hamiltonzero_amd.build)")
+    return _native.lib()
+
+
+def test_header_and_binding_agree():
+    assert header_functions() == sorted(_native.EXPORTED_SYMBOLS)
+
+
+def test_exports_every_declared_symbol(lib):
+    for name in header_functions():
+        assert hasattr(lib, name), name
+    assert _native.version() == 100
+
+
+# Fake, 256-byte aligned device addresses: every call below must fail validation on the
+# host and return before touching them.
+A = 0x10000
+
+
+def _fwd(lib, **over):
+    args = dict(stream=None, q=A, k=A, e=None, v=A, mask=A, out=A, lse=None, B=2, N=64, H=8, D=32,
+                dtype=0, scale=1.0, flags=0)
+    args.update(over)
+    return lib.hz_mhsea_fwd(*args.values())
+
+
+@pytest.mark.parametrize(
+    "over,code,needle",
+    [
+        (dict(D=24), _native.HZ_EINVAL, "head dimension"),
+        (dict(D=128), _native.HZ_EINVAL, "head dimension"),
+        (dict(N=0), _native.HZ_EINVAL, "N must be"),
+        (dict(N=_native.HZ_MAX_N + 1), _native.HZ_EINVAL, "N must be"),
+        (dict(B=0), _native.HZ_EINVAL, "B and H"),
+        (dict(dtype=7), _native.HZ_EINVAL, "dtype"),
+        (dict(flags=8), _native.HZ_EINVAL, "flag"),
+        (dict(q=None), _native.HZ_ENULL, "q must not be NULL"),
+        (dict(mask=None), _native.HZ_ENULL, "mask"),
+        (dict(out=None), _native.HZ_ENULL, "out"),
+        (dict(v=A + 4), _native.HZ_EALIGN, "aligned"),
+        (dict(scale=float("nan")), _native.HZ_EINVAL, "scale"),
+    ],
+)
+def test_fwd_rejects_bad_arguments(lib, over, code, needle):
+    assert _fwd(lib, **over) == code
+    assert needle in lib.hz_last_error().decode()
+
+
+def test_jvp_rejects_bad_tangent_count(lib):
+    rc = lib.hz_mhsea_jvp(None, A, A, None, A, A, A, A, None, None, None, None, 0, A,
+                          2, 64, 8, 32, 0, 1.0, 0)
+    assert rc == _native.HZ_EINVAL
+    assert "T must be" in lib.hz_last_error().decode()
+    rc = lib.hz_mhsea_fwd_jvp(None, A, A, None, A, A, None, None, None, None, 1, A, None, None,
+                              2, 64, 8, 32, 0, 1.0, 0)
+    assert rc == _native.HZ_ENULL and "tout" in lib.hz_last_error().decode()
+
+
+def test_jvp_requires_primal_outputs(lib):
+    rc = lib.hz_mhsea_jvp(None, A, A, None, A, A, A, None, None, None, None, None, 1, A,
+                          2, 64, 8, 32, 0, 1.0, 0)
+    assert rc == _native.HZ_ENULL and "lse" in lib.hz_last_error().decode()
+
+
+def test_bwd_rejects_missing_cotangent_outputs(lib):
+    rc = lib.hz_mhsea_bwd(None, A, A, None, A, A, A, A, A, A, None, None, A, 2, 64, 8, 32, 0, 1.0, 0)
+    assert rc == _native.HZ_ENULL and "dk" in lib.hz_last_error().decode()
+    rc = lib.hz_mhsea_bwd(None, A, A, None, A, A, A, A, A, A, A, A + 8, A, 2, 64, 8, 32, 0, 1.0, 0)
+    assert rc == _native.HZ_EALIGN and "de" in lib.hz_last_error().decode()
+
+
+def test_error_string_is_thread_local(lib):
+    import threading
+
+    assert _fwd(lib, D=24) == _native.HZ_EINVAL
+    seen = {}
+
+    def other():
+        seen["msg"] = lib.hz_last_error().decode()
+
+    t = threading.Thread(target=other)
+    t.start()
+    t.join()
+    assert seen["msg"] == ""
+    assert "head dimension" in lib.hz_last_error().decode()
+
+
+def test_check_raises_hz_error(lib):
+    assert _fwd(lib, D=24) == _native.HZ_EINVAL
+    with pytest.raises(_native.HzError) as err:
+        _native.check(_native.HZ_EINVAL)
+    assert err.value.code == _native.HZ_EINVAL
+
+
+def test_signatures_declared(lib):
+    assert lib.hz_mhsea_fwd.restype is ctypes.c_int
+    assert len(lib.hz_mhsea_jvp.argtypes) == 21
+    assert len(lib.hz_mhsea_fwd_jvp.argtypes) == 21
+    assert len(lib.hz_mhsea_bwd.argtypes) == 20

@@ -1,0 +1,207 @@
+"""GPU parity of the gfx950 MHSEA kernels against the float64 oracle (C ABI via ctypes).
+
+Tolerances (max-norm relative error, ||x - ref||_inf / ||ref||_inf per tensor):
+  float32 I/O:                 1e-5
+  bfloat16 I/O, fp32 accumulate: 2e-2, against the oracle run on the bf16-rounded inputs.
+Integer-like facts (masked rows, determinism) are checked bit-exactly.
+"""
+
+import zlib
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import mhsea_oracle as O
+
+pytestmark = pytest.mark.gpu
+
+F32_TOL = 1e-5
+BF16_TOL = 2e-2
+
+
+def _say(msg):
+    print(f"[case] {msg}", flush=True)
+
+
+def rel(a, b, floor=0.0):
+    """||a - b||_inf / max(||b||_inf, floor). ``floor`` is the magnitude of the uncancelled
+    sums behind ``b`` (used where the exact result cancels to ~0, e.g. dq at N = 1)."""
+    a = np.asarray(a, dtype=np.float64)
+    b = np.asarray(b, dtype=np.float64)
+    den = max(np.max(np.abs(b)), floor, 1e-30)
+    return float(np.max(np.abs(a - b)) / den)
+
+
+def vjp_floors(a, opts):
+    """Magnitudes of dq, dk, de without cancellation: the cotangent sums evaluated on
+    |dP| + |delta| instead of dP - delta (their rounding error scales with these)."""
+    p = O.probs(a["q"], a["k"], a["e"], a["mask"], **opts)
+    out, _ = O.fwd(a["q"], a["k"], a["e"], a["v"], a["mask"], **opts)
+    dout = np.abs(a["dout"].astype(np.float64))
+    dp = np.einsum("bihd,bjhd->bhij", dout, np.abs(a["v"].astype(np.float64)))
+    delta = np.abs(out * a["dout"]).sum(-1).transpose(0, 2, 1)[..., None]
+    ds = p * (dp + delta)
+    s = abs(opts["scale"])
+    dq = s * np.einsum("bhij,bjhd->bihd", ds, np.abs(a["k"].astype(np.float64)))
+    dk = s * np.einsum("bhij,bihd->bjhd", ds, np.abs(a["q"].astype(np.float64)))
+    return {"dq": 0.01 * dq.max(), "dk": 0.01 * dk.max(), "de": 0.01 * ds.max(), "dv": 0.0}
+
+
+def make_inputs(seed, B, N, H, D, n_phys, *, scattered=False, with_e=False, e_layout="qhk", T=1,
+                bf16=False):
+    rng = np.random.default_rng(seed)
+    shape = (B, N, H, D)
+    q, k, v = (rng.standard_normal(shape, dtype=np.float32) * np.float32(D ** -0.5) for _ in range(3))
+    eshape = (B, N, H, N) if e_layout == "qhk" else (B, N, N, H)
+    e = rng.standard_normal(eshape, dtype=np.float32) * np.float32(0.5) if with_e else None
+    tan = [rng.standard_normal((T, *shape), dtype=np.float32) for _ in range(3)]
+    et = rng.standard_normal((T, *eshape), dtype=np.float32) if with_e else None
+    dout = rng.standard_normal(shape, dtype=np.float32)
+    mask = np.zeros((B, N), dtype=bool)
+    for b in range(B):
+        sites = rng.permutation(N)[:n_phys] if scattered else np.arange(n_phys)
+        mask[b, sites] = True
+    arrs = dict(q=q, k=k, v=v, e=e, qt=tan[0], kt=tan[1], vt=tan[2], et=et, dout=dout)
+    if bf16:
+        arrs = {n: None if a is None else torch.from_numpy(a).bfloat16().float().numpy() for n, a in arrs.items()}
+    arrs["mask"] = mask
+    return arrs
+
+
+def to_dev(a, dtype):
+    if a is None:
+        return None
+    if a.dtype == bool:
+        return torch.from_numpy(a).cuda()
+    return torch.from_numpy(a).to(device="cuda", dtype=dtype)
+
+
+def host(t):
+    return None if t is None else t.float().cpu().numpy()
+
+
+CASES = [
+    # name, B, N, H, D, n_phys, scattered, with_e, e_layout, key_mask, scale, T, bf16
+    ("c1_full_fwd", 256, 8, 4, 32, 8, False, False, "qhk", False, 1.0, 1, False),
+    ("c2_small", 8, 64, 8, 32, 36, False, False, "qhk", False, 1.0, 1, False),
+    ("c2_scattered_bias", 4, 64, 4, 32, 36, True, True, "qhk", False, 1.0, 1, False),
+    ("n8_d8_bias", 6, 8, 3, 8, 5, True, True, "qhk", False, 1.0, 1, False),
+    ("n16_d16_qkh_keymask", 4, 16, 2, 16, 11, True, True, "qkh", True, 0.25, 1, False),
+    ("n96_d64_t2", 3, 96, 2, 64, 90, True, True, "qhk", False, 1.0, 2, False),
+    ("n1_d16", 5, 1, 2, 16, 1, False, False, "qhk", False, 1.0, 1, False),
+    ("n33_odd", 3, 33, 2, 32, 20, True, True, "qkh", False, 0.7, 1, False),
+    ("t3_groups", 2, 64, 2, 16, 40, True, False, "qhk", False, 1.0, 3, False),
+    ("c3_small_bf16", 4, 64, 8, 64, 48, False, False, "qhk", False, 1.0, 1, True),
+    ("c4_small", 2, 256, 4, 64, 225, False, False, "qhk", False, 1.0, 1, False),
+    ("c5_small_bf16", 1, 1024, 2, 64, 1000, False, False, "qhk", False, 1.0, 2, True),
+    ("keymask_all_masked", 3, 16, 2, 32, 0, False, True, "qkh", True, 1.0, 1, False),
+    ("square_all_masked", 3, 16, 2, 32, 0, False, True, "qhk", False, 1.0, 1, False),
+]
+IDS = [c[0] for c in CASES]
+
+
+def _setup(case):
+    name, B, N, H, D, n_phys, scattered, with_e, e_layout, key_mask, scale, T, bf16 = case
+    a = make_inputs(zlib.crc32(name.encode()) % 1000, B, N, H, D, n_phys, scattered=scattered, with_e=with_e,
+                    e_layout=e_layout, T=T, bf16=bf16)
+    dt = torch.bfloat16 if bf16 else torch.float32
+    d = {n: to_dev(x, dt) for n, x in a.items()}
+    opts = dict(scale=scale, key_mask=key_mask, e_layout=e_layout)
+    tol = BF16_TOL if bf16 else F32_TOL
+    return a, d, opts, tol, T
+
+
+@pytest.mark.parametrize("case", CASES, ids=IDS)
+def test_fwd_parity(case):
+    from hamiltonzero_amd import kernels
+
+    _say(f"fwd {case[0]}")
+    a, d, opts, tol, _ = _setup(case)
+    out, lse = kernels.mhsea_fwd(d["q"], d["k"], d["v"], d["mask"], d["e"], **opts)
+    torch.cuda.synchronize()
+    ref_out, ref_lse = O.fwd(a["q"], a["k"], a["e"], a["v"], a["mask"], **opts)
+    assert rel(host(out), ref_out) <= tol
+    m = a["mask"]
+    has_key = m.any(axis=1)
+    if not opts["key_mask"]:
+        assert np.all(host(out)[~m] == 0.0)
+        assert rel(host(lse)[m], ref_lse[m]) <= tol if m.any() else True
+        np.testing.assert_allclose(host(lse)[~m], ref_lse[~m], rtol=1e-6)
+    else:
+        sel = has_key
+        if sel.any():
+            assert rel(host(lse)[sel], ref_lse[sel]) <= tol
+
+
+@pytest.mark.parametrize("case", CASES, ids=IDS)
+def test_fwd_jvp_parity(case):
+    from hamiltonzero_amd import kernels
+
+    _say(f"fwd_jvp {case[0]}")
+    a, d, opts, tol, T = _setup(case)
+    out, lse, tout = kernels.mhsea_fwd_jvp(d["q"], d["k"], d["v"], d["mask"], d["qt"], d["kt"], d["vt"],
+                                           d["e"], d["et"], **opts)
+    torch.cuda.synchronize()
+    ref_out, _ = O.fwd(a["q"], a["k"], a["e"], a["v"], a["mask"], **opts)
+    assert rel(host(out), ref_out) <= tol
+    for t in range(T):
+        et = None if a["et"] is None else a["et"][t]
+        ref_t = O.jvp(a["q"], a["k"], a["e"], a["v"], a["mask"], a["qt"][t], a["kt"][t], et, a["vt"][t], **opts)
+        got = host(tout)[t]
+        assert rel(got, ref_t) <= tol, f"tangent {t}"
+        if not opts["key_mask"]:
+            assert np.all(got[~a["mask"]] == 0.0)
+
+
+@pytest.mark.parametrize("case", CASES, ids=IDS)
+def test_jvp_given_lse_parity(case):
+    from hamiltonzero_amd import kernels
+
+    _say(f"jvp {case[0]}")
+    a, d, opts, tol, T = _setup(case)
+    out, lse = kernels.mhsea_fwd(d["q"], d["k"], d["v"], d["mask"], d["e"], **opts)
+    tout = kernels.mhsea_jvp(d["q"], d["k"], d["v"], d["mask"], out, lse, d["qt"], d["kt"], d["vt"],
+                             d["e"], d["et"], **opts)
+    torch.cuda.synchronize()
+    for t in range(T):
+        et = None if a["et"] is None else a["et"][t]
+        ref_t = O.jvp(a["q"], a["k"], a["e"], a["v"], a["mask"], a["qt"][t], a["kt"][t], et, a["vt"][t], **opts)
+        assert rel(host(tout)[t], ref_t) <= tol, f"tangent {t}"
+
+
+@pytest.mark.parametrize("case", CASES, ids=IDS)
+def test_bwd_parity(case):
+    from hamiltonzero_amd import kernels
+
+    _say(f"bwd {case[0]}")
+    a, d, opts, tol, _ = _setup(case)
+    out, lse = kernels.mhsea_fwd(d["q"], d["k"], d["v"], d["mask"], d["e"], **opts)
+    dq, dk, de, dv = kernels.mhsea_bwd(d["q"], d["k"], d["v"], d["mask"], lse, out, d["dout"], d["e"],
+                                       want_de=True, **opts)
+    torch.cuda.synchronize()
+    ref = O.vjp(a["q"], a["k"], a["e"], a["v"], a["mask"], a["dout"], **opts)
+    floors = vjp_floors(a, opts)
+    for name, got, want in zip(("dq", "dk", "de", "dv"), (dq, dk, de, dv), ref):
+        if np.max(np.abs(want)) == 0.0 and floors[name] == 0.0:
+            assert np.all(host(got) == 0.0), name
+        else:
+            assert rel(host(got), want, floors[name]) <= tol, name
+    m = a["mask"]
+    if not opts["key_mask"]:
+        for name, got in (("dq", dq), ("dk", dk), ("dv", dv)):
+            assert np.all(host(got)[~m] == 0.0), name
+
+
+def test_deterministic_bitwise():
+    from hamiltonzero_amd import kernels
+
+    _say("determinism c2 small")
+    a = make_inputs(5, 16, 64, 8, 32, 36, with_e=True)
+    d = {n: to_dev(x, torch.float32) for n, x in a.items()}
+    r1 = kernels.mhsea_fwd_jvp(d["q"], d["k"], d["v"], d["mask"], d["qt"], d["kt"], d["vt"], d["e"], d["et"])
+    r2 = kernels.mhsea_fwd_jvp(d["q"], d["k"], d["v"], d["mask"], d["qt"], d["kt"], d["vt"], d["e"], d["et"])
+    g1 = kernels.mhsea_bwd(d["q"], d["k"], d["v"], d["mask"], r1[1], r1[0], d["dout"], d["e"])
+    g2 = kernels.mhsea_bwd(d["q"], d["k"], d["v"], d["mask"], r1[1], r1[0], d["dout"], d["e"])
+    for x, y in zip((*r1, *g1), (*r2, *g2)):
+        assert torch.equal(x, y)
