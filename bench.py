@@ -102,6 +102,8 @@ def main(argv=None):
     ap.add_argument("--config", default="c2", choices=sorted(CONFIGS))
     ap.add_argument("--cpu-budget", type=float, default=15.0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--generic", action="store_true",
+                    help="force the LDS-streaming kernels (HZ_FLAG_GENERIC) for comparison")
     args = ap.parse_args(argv)
 
     if args.gpus != 1:
@@ -142,11 +144,12 @@ def main(argv=None):
     s = stream.cuda_stream
     out = torch.empty(shape, dtype=tdt, device=dev)
     P = lambda t: None if t is None else t.data_ptr()  # noqa: E731
+    fl = _native.HZ_FLAG_GENERIC if args.generic else 0
 
     if work == "fwd":
         def step():
             _native.check(lib.hz_mhsea_fwd(s, P(q), P(k), None, P(v), P(mask), P(out), None,
-                                           B, N, H, D, hz_dtype, 1.0, 0))
+                                           B, N, H, D, hz_dtype, 1.0, fl))
     elif work == "fwd_jvp":
         qt = torch.stack([t[0] for t in tans]).contiguous()
         kt = torch.stack([t[1] for t in tans]).contiguous()
@@ -156,16 +159,16 @@ def main(argv=None):
 
         def step():
             _native.check(lib.hz_mhsea_fwd_jvp(s, P(q), P(k), None, P(v), P(mask), P(qt), P(kt), None, P(vt), T,
-                                               P(out), None, P(tout), B, N, H, D, hz_dtype, 1.0, 0))
+                                               P(out), None, P(tout), B, N, H, D, hz_dtype, 1.0, fl))
     else:
         lse = torch.empty((B, N, H), dtype=torch.float32, device=dev)
         dq, dk, dv = (torch.empty(shape, dtype=tdt, device=dev) for _ in range(3))
 
         def step():
             _native.check(lib.hz_mhsea_fwd(s, P(q), P(k), None, P(v), P(mask), P(out), P(lse),
-                                           B, N, H, D, hz_dtype, 1.0, 0))
+                                           B, N, H, D, hz_dtype, 1.0, fl))
             _native.check(lib.hz_mhsea_bwd(s, P(q), P(k), None, P(v), P(mask), P(lse), P(out), P(dout),
-                                           P(dq), P(dk), None, P(dv), B, N, H, D, hz_dtype, 1.0, 0))
+                                           P(dq), P(dk), None, P(dv), B, N, H, D, hz_dtype, 1.0, fl))
 
     for _ in range(args.warmup):
         step()
@@ -223,7 +226,8 @@ def main(argv=None):
         "dtype": "bf16" if dtype == "bf16" else "f32",
         "data": "synthetic (numpy default_rng, N(0,1)/sqrt(D) q/k/v, N(0,1) tangents)",
         "config": {"workload": f"{args.config}: {desc}", "B": B, "N": N, "H": H, "D": D,
-                   "n_phys": n_phys, "T": T, "work": work},
+                   "n_phys": n_phys, "T": T, "work": work,
+                   "kernels": "generic" if args.generic else "auto"},
         "roofline": roof,
         "roofline_padded": roof_padded,
         "cpu_baseline": cpu,

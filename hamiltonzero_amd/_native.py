@@ -16,6 +16,7 @@ HZ_DTYPE_F32 = 0
 HZ_DTYPE_BF16 = 1
 HZ_FLAG_KEY_MASK = 1
 HZ_FLAG_E_QKH = 2
+HZ_FLAG_GENERIC = 4
 HZ_MAX_N = 16384
 
 HZ_OK = 0

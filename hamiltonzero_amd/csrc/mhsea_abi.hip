@@ -37,7 +37,7 @@ int check_dims(int64_t B, int64_t N, int64_t H, int64_t D, int dtype, int flags)
     return fail(HZ_EINVAL, "head dimension must be one of [8, 16, 32, 64], got %lld", (long long)D);
   if (dtype != HZ_DTYPE_F32 && dtype != HZ_DTYPE_BF16)
     return fail(HZ_EINVAL, "dtype must be HZ_DTYPE_F32 (0) or HZ_DTYPE_BF16 (1), got %d", dtype);
-  if (flags & ~(HZ_FLAG_KEY_MASK | HZ_FLAG_E_QKH)) return fail(HZ_EINVAL, "unknown flag bits 0x%x", flags);
+  if (flags & ~(HZ_FLAG_KEY_MASK | HZ_FLAG_E_QKH | HZ_FLAG_GENERIC)) return fail(HZ_EINVAL, "unknown flag bits 0x%x", flags);
   const int64_t nwg = B * H * ((N + 63) / 64);
   if (nwg > 0x7fffffffLL) return fail(HZ_EINVAL, "B*H*ceil(N/64) = %lld exceeds the grid limit", (long long)nwg);
   if (B * N * H * N > (int64_t(1) << 46))
@@ -94,6 +94,7 @@ hz::FwdParams fwd_params(const void* q, const void* k, const void* e, const void
   p.scale = scale;
   p.key_mask = (flags & HZ_FLAG_KEY_MASK) ? 1 : 0;
   p.masked_lse = -10000.0f + std::log(static_cast<float>(N));
+  p.force_generic = (flags & HZ_FLAG_GENERIC) ? 1 : 0;
   return p;
 }
 

@@ -28,6 +28,11 @@ __device__ __forceinline__ v4f mfma16x4(float a, float b, v4f c) {
 
 __device__ __forceinline__ v4f zero4() { return v4f{0.f, 0.f, 0.f, 0.f}; }
 
+// 2^x with the hardware transcendental (v_exp_f32, ~1 ulp). Results below the float32
+// normal range may flush to zero, which only affects softmax weights < 2^-126 relative to
+// the row maximum.
+__device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
+
 // bfloat16 <-> float32. Round-to-nearest-even on the way down; NaN stays NaN.
 __device__ __forceinline__ float bf16_to_f32(uint16_t x) {
   return __uint_as_float(static_cast<uint32_t>(x) << 16);
@@ -152,6 +157,65 @@ __device__ __forceinline__ int compact_mask(const uint8_t* __restrict__ mask_row
     for (int w = 0; w < wave; ++w) before += scratch[w];
     const int mine = __popcll(bal & ((uint64_t(1) << lane) - 1));
     if (on) idx[before + mine] = static_cast<int16_t>(pos);
+    total += scratch[0] + scratch[1] + scratch[2] + scratch[3];
+    __syncthreads();
+  }
+  return total;
+}
+
+// Per-walker compaction of the mask, one global round trip per 4096 sites: each thread
+// reads 16 consecutive mask bytes, a workgroup-wide scan of the per-thread counts places
+// the physical sites in idx[0..count) (ascending), and the raw bytes are kept in mask_s
+// for later tests without touching global memory again. Returns count to every thread.
+// Must be called by all threads of a 256-thread workgroup; `scratch` holds 4 ints;
+// mask_s must be 16-byte aligned.
+__device__ __forceinline__ int compact_mask_lds(const uint8_t* __restrict__ mask_row, int N,
+                                                int16_t* __restrict__ idx,
+                                                uint8_t* __restrict__ mask_s,
+                                                int* __restrict__ scratch) {
+  const int tid = threadIdx.x;
+  const int wave = tid >> 6;
+  const int lane = tid & 63;
+  const bool vec = (reinterpret_cast<uintptr_t>(mask_row) & 15u) == 0;
+  int total = 0;
+  for (int base = 0; base < N; base += 4096) {
+    const int s0 = base + tid * 16;
+    uint32_t bits = 0;
+    if (vec && s0 + 16 <= N) {
+      const uint4 w = *reinterpret_cast<const uint4*>(mask_row + s0);
+      *reinterpret_cast<uint4*>(mask_s + s0) = w;
+      const uint32_t words[4] = {w.x, w.y, w.z, w.w};
+#pragma unroll
+      for (int q = 0; q < 4; ++q)
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+          bits |= (((words[q] >> (8 * i)) & 0xffu) != 0u ? 1u : 0u) << (4 * q + i);
+    } else {
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        if (s0 + i < N) {
+          const uint8_t m = mask_row[s0 + i];
+          mask_s[s0 + i] = m;
+          bits |= (m != 0 ? 1u : 0u) << i;
+        }
+      }
+    }
+    const int cnt = __popc(bits);
+    int incl = cnt;
+#pragma unroll
+    for (int d = 1; d < 64; d <<= 1) {
+      const int y = __shfl_up(incl, d, 64);
+      if (lane >= d) incl += y;
+    }
+    if (lane == 63) scratch[wave] = incl;
+    __syncthreads();
+    int pos = total + incl - cnt;
+    for (int w = 0; w < wave; ++w) pos += scratch[w];
+    while (bits != 0u) {
+      const int i = __ffs(bits) - 1;
+      idx[pos++] = static_cast<int16_t>(s0 + i);
+      bits &= bits - 1u;
+    }
     total += scratch[0] + scratch[1] + scratch[2] + scratch[3];
     __syncthreads();
   }

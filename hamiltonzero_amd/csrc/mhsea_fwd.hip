@@ -33,10 +33,15 @@ struct FwdShape {
   static constexpr int LD = D + 4;                         // padded LDS row, floats
   static constexpr int DG = D / 4;   // contraction values per lane group in K.Q^T
   static constexpr int DT = (D + 15) / 16;  // 16-row tiles of O^T
+  static constexpr int C4 = D / 4;          // float4 columns of one row
   static constexpr int NT = 2 + 2 * T;      // staged tensors: K, V, Kt[T], Vt[T]
+  static constexpr int TT = T > 0 ? T : 1;
   static constexpr int kTileFloats = KC * LD;
+  static constexpr int kItems = KC * C4;                 // float4 items per tensor chunk
+  static constexpr int kPerThread = (kItems + 255) / 256;
   static size_t lds_bytes(int N) {
-    return static_cast<size_t>(NT) * kTileFloats * 4 + 8 * 4 + ((static_cast<size_t>(N) * 2 + 15) & ~size_t(15));
+    const size_t n16 = (static_cast<size_t>(N) + 15) & ~size_t(15);
+    return static_cast<size_t>(NT) * kTileFloats * 4 + 16 + n16 /*mask*/ + 2 * n16 /*idx*/;
   }
 };
 
@@ -58,11 +63,69 @@ __device__ __forceinline__ void load_row_frag(const void* base, int64_t off, flo
   }
 }
 
-template <int D, int T, bool GIVEN_LSE, bool HAS_E, class S>
-__global__ void __launch_bounds__(256) mhsea_fwd_kernel(const FwdParams p) {
+// Issue the global loads of key rows [kc, kc + KC) of the compacted list into registers
+// (K, V and the tangent keys / values). Every load is unconditional from an in-bounds row
+// (site 0 stands in for padding) so that all of them are in flight before the first wait;
+// padding is zeroed when the chunk is written to LDS.
+template <int D, int T, class S, int NPT, int TT>
+__device__ __forceinline__ void chunk_load(float4 (&ck)[NPT], float4 (&cv)[NPT],
+                                           float4 (&ckt)[TT][NPT], float4 (&cvt)[TT][NPT],
+                                           const FwdParams& p, int b, int h, int kc, int nk,
+                                           bool key_all, const int16_t* idx, const void* ktp,
+                                           int64_t kts, const void* vtp, int64_t vts) {
   using Sh = FwdShape<D, T>;
-  constexpr int KC = Sh::KC, LD = Sh::LD, DG = Sh::DG, DT = Sh::DT;
-  constexpr int C4 = D / 4;
+#pragma unroll
+  for (int u = 0; u < Sh::kPerThread; ++u) {
+    const int it = threadIdx.x + u * 256;
+    const int j = kc + it / Sh::C4;
+    const bool ok = (Sh::kItems % 256 == 0 || it < Sh::kItems) && j < nk;
+    const int n = ok ? (key_all ? j : idx[j]) : 0;
+    const int64_t off = bnhd(b, n, h, p.N, p.H, D) + (it % Sh::C4) * 4;
+    ck[u] = load4<S>(p.k, off);
+    cv[u] = load4<S>(p.v, off);
+#pragma unroll
+    for (int t = 0; t < T; ++t) {
+      ckt[t][u] = load4<S>(ktp, t * kts + off);
+      cvt[t][u] = load4<S>(vtp, t * vts + off);
+    }
+  }
+}
+
+__device__ __forceinline__ void put4(float* dst, float4 x, bool keep) {
+  *reinterpret_cast<float4*>(dst) =
+      make_float4(keep ? x.x : 0.f, keep ? x.y : 0.f, keep ? x.z : 0.f, keep ? x.w : 0.f);
+}
+
+template <int D, int T, int NPT, int TT>
+__device__ __forceinline__ void chunk_store(const float4 (&ck)[NPT], const float4 (&cv)[NPT],
+                                            const float4 (&ckt)[TT][NPT], const float4 (&cvt)[TT][NPT],
+                                            float* Ks, int kc, int nk, bool has_kt, bool has_vt) {
+  using Sh = FwdShape<D, T>;
+#pragma unroll
+  for (int u = 0; u < Sh::kPerThread; ++u) {
+    const int it = threadIdx.x + u * 256;
+    if (Sh::kItems % 256 == 0 || it < Sh::kItems) {
+      const int r = it / Sh::C4;
+      const bool ok = kc + r < nk;
+      const int so = r * Sh::LD + (it % Sh::C4) * 4;
+      put4(Ks + so, ck[u], ok);
+      put4(Ks + Sh::kTileFloats + so, cv[u], ok);
+#pragma unroll
+      for (int t = 0; t < T; ++t) {
+        put4(Ks + (2 + t) * Sh::kTileFloats + so, ckt[t][u], ok && has_kt);
+        put4(Ks + (2 + T + t) * Sh::kTileFloats + so, cvt[t][u], ok && has_vt);
+      }
+    }
+  }
+}
+
+// MULTI: N > KC, so keys arrive in several chunks (register prefetch of the next chunk,
+// online rescaling between chunks); otherwise the single chunk holds every key.
+template <int D, int T, bool GIVEN_LSE, bool HAS_E, class S, bool MULTI>
+__global__ void __launch_bounds__(256, (D == 64 && T > 0) ? 2 : 3) mhsea_fwd_kernel(const FwdParams p) {
+  using Sh = FwdShape<D, T>;
+  constexpr int KC = Sh::KC, LD = Sh::LD, DG = Sh::DG, DT = Sh::DT, C4 = Sh::C4, TT = Sh::TT;
+  constexpr int NJT = KC / 16;  // 16-key tiles per chunk
 
   extern __shared__ float4 smem4[];
   float* const Ks = reinterpret_cast<float*>(smem4);
@@ -70,7 +133,9 @@ __global__ void __launch_bounds__(256) mhsea_fwd_kernel(const FwdParams p) {
   float* const Kts = Vs + Sh::kTileFloats;
   float* const Vts = Kts + T * Sh::kTileFloats;
   int* const scratch = reinterpret_cast<int*>(Ks + Sh::NT * Sh::kTileFloats);
-  int16_t* const idx = reinterpret_cast<int16_t*>(scratch + 8);
+  const int n16 = (p.N + 15) & ~15;
+  uint8_t* const mask_s = reinterpret_cast<uint8_t*>(scratch + 4);
+  int16_t* const idx = reinterpret_cast<int16_t*>(mask_s + n16);
 
   const int N = p.N, H = p.H;
   const int nblk = (N + 63) >> 6;
@@ -86,67 +151,54 @@ __global__ void __launch_bounds__(256) mhsea_fwd_kernel(const FwdParams p) {
   const int g = lane >> 4;
   const int c = lane & 15;
 
-  const uint8_t* mrow = p.mask + static_cast<int64_t>(b) * N;
-  const int n_phys = compact_mask(mrow, N, idx, scratch);
+  const int n_phys = compact_mask_lds(p.mask + static_cast<int64_t>(b) * N, N, idx, mask_s, scratch);
   const bool key_all = p.key_mask && n_phys == 0;
   const int nk = key_all ? N : n_phys;
   const int nq = p.key_mask ? N : n_phys;
 
-  // Rows of masked queries (square mask only) are exact zeros; lse takes the value the
-  // reference's all -1e4 row produces, -1e4 + log(N).
-  if (!p.key_mask) {
-    const int r0 = blk * 64;
-    for (int it = tid; it < 64 * C4; it += 256) {
-      const int r = r0 + it / C4;
-      const int c4 = it % C4;
-      if (r < N && mrow[r] == 0) {
-        const int64_t off = bnhd(b, r, h, N, H, D) + c4 * 4;
-        if constexpr (!GIVEN_LSE) store4<S>(p.out, off, 0.f, 0.f, 0.f, 0.f);
-#pragma unroll
-        for (int t = 0; t < T; ++t) store4<S>(p.tout, t * p.t_stride + off, 0.f, 0.f, 0.f, 0.f);
-        if (!GIVEN_LSE && c4 == 0 && p.lse != nullptr)
-          p.lse[(static_cast<int64_t>(b) * N + r) * H + h] = p.masked_lse;
-      }
-    }
-  }
+  // A null tangent pointer is replaced by its primal (always readable); the values are
+  // discarded when written to LDS / registers.
+  const bool has_kt = p.kt != nullptr, has_vt = p.vt != nullptr, has_qt = p.qt != nullptr;
+  const void* const ktp = has_kt ? p.kt : p.k;
+  const void* const vtp = has_vt ? p.vt : p.v;
+  const void* const qtp = has_qt ? p.qt : p.q;
+  const int64_t kts = has_kt ? p.t_stride : 0, vts = has_vt ? p.t_stride : 0;
+  const int64_t qts = has_qt ? p.t_stride : 0;
+
+  // ---- issue every global load of the prologue before the first wait ---------------
+  constexpr int NPT = Sh::kPerThread;
+  float4 ck[NPT], cv[NPT], ckt[TT][NPT], cvt[TT][NPT];
+  chunk_load<D, T, S, NPT, TT>(ck, cv, ckt, cvt, p, b, h, 0, nk, key_all, idx, ktp, kts, vtp, vts);
 
   const int q0 = blk * 64 + wave * 16;
   const bool active = q0 < nq;  // wave-uniform
-  int qsite = -1;
-  if (q0 + c < nq) qsite = p.key_mask ? (q0 + c) : idx[q0 + c];
+  const bool qvalid = q0 + c < nq;
+  const int qsite = qvalid ? (p.key_mask ? (q0 + c) : idx[q0 + c]) : -1;
+  const int qload = qvalid ? qsite : 0;
+  const float qscale = qvalid ? p.scale : 0.f;
+  const float qtscale = has_qt ? qscale : 0.f;
 
   // Query fragment in B-operand layout: lane (g, c) holds q[qsite][g*DG .. g*DG+DG).
   float qf[DG];
-  float qtf[T > 0 ? T : 1][DG];
+  float qtf[TT][DG];
   float lse2 = 0.f;
+  const int64_t qoff = bnhd(b, qload, h, N, H, D) + g * DG;
+  load_row_frag<DG, S>(p.q, qoff, qf);
 #pragma unroll
-  for (int s = 0; s < DG; ++s) qf[s] = 0.f;
+  for (int t = 0; t < T; ++t) load_row_frag<DG, S>(qtp, t * qts + qoff, qtf[t]);
+  if constexpr (GIVEN_LSE) lse2 = p.lse_in[(static_cast<int64_t>(b) * N + qload) * H + h] * kLog2e;
 #pragma unroll
-  for (int t = 0; t < T; ++t)
+  for (int s = 0; s < DG; ++s) {
+    qf[s] *= qscale;
 #pragma unroll
-    for (int s = 0; s < DG; ++s) qtf[t][s] = 0.f;
-  if (qsite >= 0) {
-    const int64_t off = bnhd(b, qsite, h, N, H, D) + g * DG;
-    load_row_frag<DG, S>(p.q, off, qf);
-#pragma unroll
-    for (int s = 0; s < DG; ++s) qf[s] *= p.scale;
-    if (p.qt != nullptr) {
-#pragma unroll
-      for (int t = 0; t < T; ++t) {
-        load_row_frag<DG, S>(p.qt, t * p.t_stride + off, qtf[t]);
-#pragma unroll
-        for (int s = 0; s < DG; ++s) qtf[t][s] *= p.scale;
-      }
-    }
-    if constexpr (GIVEN_LSE) lse2 = p.lse_in[(static_cast<int64_t>(b) * N + qsite) * H + h] * kLog2e;
+    for (int t = 0; t < T; ++t) qtf[t][s] *= qtscale;
   }
-  const int64_t e_row = static_cast<int64_t>(b) * N * N * H +
-                        static_cast<int64_t>(qsite < 0 ? 0 : qsite) * p.e_sq +
+  const int64_t e_row = static_cast<int64_t>(b) * N * N * H + static_cast<int64_t>(qload) * p.e_sq +
                         static_cast<int64_t>(h) * p.e_sh;
 
   v4f o[DT];
-  v4f at[T > 0 ? T : 1][DT];
-  v4f ct[T > 0 ? T : 1][DT];
+  v4f at[TT][DT];
+  v4f ct[TT][DT];
 #pragma unroll
   for (int dt = 0; dt < DT; ++dt) {
     o[dt] = zero4();
@@ -156,99 +208,91 @@ __global__ void __launch_bounds__(256) mhsea_fwd_kernel(const FwdParams p) {
       ct[t][dt] = zero4();
     }
   }
-  float m2 = -INFINITY;  // running max of the base-2 scores
+  float m2 = -INFINITY;  // running max of the base-2 scores (uniform over a lane column)
   float lsum = 0.f;      // this lane's share of the softmax normaliser
-  float mu[T > 0 ? T : 1];
+  float mu[TT];
 #pragma unroll
   for (int t = 0; t < T; ++t) mu[t] = 0.f;
 
   for (int kc = 0; kc < nk; kc += KC) {
-    __syncthreads();  // previous chunk fully consumed
-    for (int it = tid; it < KC * C4; it += 256) {
-      const int r = it / C4;
-      const int c4 = it % C4;
-      const int j = kc + r;
-      float4 kx = make_float4(0.f, 0.f, 0.f, 0.f), vx = kx;
-      float4 ktx[T > 0 ? T : 1], vtx[T > 0 ? T : 1];
-#pragma unroll
-      for (int t = 0; t < T; ++t) ktx[t] = vtx[t] = kx;
-      if (j < nk) {
-        const int n = key_all ? j : idx[j];
-        const int64_t off = bnhd(b, n, h, N, H, D) + c4 * 4;
-        kx = load4<S>(p.k, off);
-        vx = load4<S>(p.v, off);
-#pragma unroll
-        for (int t = 0; t < T; ++t) {
-          if (p.kt != nullptr) ktx[t] = load4<S>(p.kt, t * p.t_stride + off);
-          if (p.vt != nullptr) vtx[t] = load4<S>(p.vt, t * p.t_stride + off);
-        }
-      }
-      const int so = r * LD + c4 * 4;
-      *reinterpret_cast<float4*>(Ks + so) = kx;
-      *reinterpret_cast<float4*>(Vs + so) = vx;
-#pragma unroll
-      for (int t = 0; t < T; ++t) {
-        *reinterpret_cast<float4*>(Kts + t * Sh::kTileFloats + so) = ktx[t];
-        *reinterpret_cast<float4*>(Vts + t * Sh::kTileFloats + so) = vtx[t];
-      }
-    }
+    if (kc > 0) __syncthreads();  // every wave is done with the previous chunk
+    chunk_store<D, T, NPT, TT>(ck, cv, ckt, cvt, Ks, kc, nk, has_kt, has_vt);
     __syncthreads();
+    if constexpr (MULTI) {
+      if (kc + KC < nk)
+        chunk_load<D, T, S, NPT, TT>(ck, cv, ckt, cvt, p, b, h, kc + KC, nk, key_all, idx, ktp, kts, vtp, vts);
+    }
     if (!active) continue;
 
+    // The whole chunk at once: scores of every 16-key tile, one max, one rescale of the
+    // accumulators per chunk (none for the first), then the P.V products.
     const int jn = min(KC, nk - kc);
-    for (int jt = 0; jt * 16 < jn; ++jt) {
-      // ---- scores S^T[key 4g+r][query c] and their tangents -------------------------
-      const float* krow = Ks + (jt * 16 + c) * LD + g * DG;
-      v4f sc = zero4();
+    const int njt = (jn + 15) >> 4;
+    v4f sc[NJT];
+    v4f ds[TT][NJT];
 #pragma unroll
-      for (int s = 0; s < DG; ++s) sc = mfma16x4(krow[s], qf[s], sc);
-      v4f ds[T > 0 ? T : 1];
+    for (int jt = 0; jt < NJT; ++jt) {
+      sc[jt] = zero4();
 #pragma unroll
-      for (int t = 0; t < T; ++t) {
-        const float* ktrow = Kts + t * Sh::kTileFloats + (jt * 16 + c) * LD + g * DG;
-        ds[t] = zero4();
+      for (int t = 0; t < T; ++t) ds[t][jt] = zero4();
+    }
+    // One tile at a time (the scheduling fences keep the next tile's LDS reads from being
+    // hoisted, which would multiply the live registers).
+#pragma unroll
+    for (int jt = 0; jt < NJT; ++jt) {
+      if (jt < njt) {
+        const float* krow = Ks + (jt * 16 + c) * LD + g * DG;
 #pragma unroll
         for (int s = 0; s < DG; ++s) {
-          ds[t] = mfma16x4(ktrow[s], qf[s], ds[t]);
-          ds[t] = mfma16x4(krow[s], qtf[t][s], ds[t]);
+          const float kv = krow[s];
+          sc[jt] = mfma16x4(kv, qf[s], sc[jt]);
+#pragma unroll
+          for (int t = 0; t < T; ++t) {
+            const float ktv = krow[(2 + t) * Sh::kTileFloats + s];
+            ds[t][jt] = mfma16x4(ktv, qf[s], ds[t][jt]);
+            ds[t][jt] = mfma16x4(kv, qtf[t][s], ds[t][jt]);
+          }
         }
       }
+      __builtin_amdgcn_sched_barrier(0);
+    }
 
-      float s2[4];
+    float mx = -INFINITY;
+#pragma unroll
+    for (int jt = 0; jt < NJT; ++jt) {
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
         const int j = kc + jt * 16 + 4 * g + r;
-        const bool valid = j < nk;
-        float sv = sc[r];
-        if (HAS_E || p.et != nullptr) {
-          if (valid && qsite >= 0) {
-            const int n = key_all ? j : idx[j];
-            const int64_t eo = e_row + static_cast<int64_t>(n) * p.e_sk;
-            if constexpr (HAS_E) sv += load1<S>(p.e, eo);
+        const bool valid = jt < njt && j < nk;
+        float sv = sc[jt][r];
+        if constexpr (HAS_E) {
+          if (valid) {
+            const int64_t eo = e_row + static_cast<int64_t>(key_all ? j : idx[j]) * p.e_sk;
+            if (p.e != nullptr) sv += load1<S>(p.e, eo);
             if (p.et != nullptr) {
 #pragma unroll
-              for (int t = 0; t < T; ++t) ds[t][r] += load1<S>(p.et, t * p.et_stride + eo);
+              for (int t = 0; t < T; ++t) ds[t][jt][r] += load1<S>(p.et, t * p.et_stride + eo);
             }
           }
         }
-        s2[r] = valid ? sv * kLog2e : -INFINITY;
+        sc[jt][r] = valid ? sv * kLog2e : -INFINITY;
 #pragma unroll
-        for (int t = 0; t < T; ++t) ds[t][r] = valid ? ds[t][r] : 0.f;
+        for (int t = 0; t < T; ++t) ds[t][jt][r] = valid ? ds[t][jt][r] : 0.f;
+        mx = fmaxf(mx, sc[jt][r]);
       }
+    }
 
-      // ---- softmax weights --------------------------------------------------------
-      float pr[4];
-      if constexpr (GIVEN_LSE) {
+    // sc becomes the (unnormalised) softmax weight in place.
+    if constexpr (GIVEN_LSE) {
 #pragma unroll
-        for (int r = 0; r < 4; ++r) pr[r] = exp2f(s2[r] - lse2);
-      } else {
-        const float mx = group_max(fmaxf(fmaxf(s2[0], s2[1]), fmaxf(s2[2], s2[3])));
-        const float mnew = fmaxf(m2, mx);
-        const float alpha = exp2f(m2 - mnew);
-        m2 = mnew;
+      for (int jt = 0; jt < NJT; ++jt)
 #pragma unroll
-        for (int r = 0; r < 4; ++r) pr[r] = exp2f(s2[r] - mnew);
-        lsum = lsum * alpha + ((pr[0] + pr[1]) + (pr[2] + pr[3]));
+        for (int r = 0; r < 4; ++r) sc[jt][r] = fast_exp2(sc[jt][r] - lse2);
+    } else {
+      const float mnew = fmaxf(m2, group_max(mx));
+      if (MULTI && kc > 0) {
+        const float alpha = fast_exp2(m2 - mnew);
+        lsum *= alpha;
 #pragma unroll
         for (int dt = 0; dt < DT; ++dt) {
           o[dt] *= alpha;
@@ -261,75 +305,110 @@ __global__ void __launch_bounds__(256) mhsea_fwd_kernel(const FwdParams p) {
 #pragma unroll
         for (int t = 0; t < T; ++t) mu[t] *= alpha;
       }
-      float pds[T > 0 ? T : 1][4];
+      m2 = mnew;
 #pragma unroll
-      for (int t = 0; t < T; ++t) {
+      for (int jt = 0; jt < NJT; ++jt)
 #pragma unroll
-        for (int r = 0; r < 4; ++r) pds[t][r] = pr[r] * ds[t][r];
-        mu[t] += (pds[t][0] + pds[t][1]) + (pds[t][2] + pds[t][3]);
+        for (int r = 0; r < 4; ++r) {
+          sc[jt][r] = fast_exp2(sc[jt][r] - m2);
+          lsum += sc[jt][r];
+        }
+    }
+    // ds becomes P o dS in place.
+#pragma unroll
+    for (int t = 0; t < T; ++t)
+#pragma unroll
+      for (int jt = 0; jt < NJT; ++jt) {
+        ds[t][jt] *= sc[jt];
+        mu[t] += (ds[t][jt][0] + ds[t][jt][1]) + (ds[t][jt][2] + ds[t][jt][3]);
       }
 
-      // ---- O^T += V^T P^T ;  A^T += V^T (P o dS)^T ;  C^T += Vt^T P^T ----------------
+    // ---- O^T += V^T P^T ;  A^T += V^T (P o dS)^T ;  C^T += Vt^T P^T ------------------
 #pragma unroll
-      for (int dt = 0; dt < DT; ++dt) {
-        const int col = dt * 16 + c;
+    for (int jt = 0; jt < NJT; ++jt) {
+      if (jt < njt) {
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
           const int row = jt * 16 + 4 * g + r;
-          const float va = (D % 16 == 0 || col < D) ? Vs[row * LD + col] : 0.f;
-          if constexpr (!GIVEN_LSE) o[dt] = mfma16x4(va, pr[r], o[dt]);
 #pragma unroll
-          for (int t = 0; t < T; ++t) {
-            at[t][dt] = mfma16x4(va, pds[t][r], at[t][dt]);
-            const float vta =
-                (D % 16 == 0 || col < D) ? Vts[t * Sh::kTileFloats + row * LD + col] : 0.f;
-            ct[t][dt] = mfma16x4(vta, pr[r], ct[t][dt]);
+          for (int dt = 0; dt < DT; ++dt) {
+            const int col = dt * 16 + c;
+            const float va = (D % 16 == 0 || col < D) ? Vs[row * LD + col] : 0.f;
+            if constexpr (!GIVEN_LSE) o[dt] = mfma16x4(va, sc[jt][r], o[dt]);
+#pragma unroll
+            for (int t = 0; t < T; ++t) {
+              at[t][dt] = mfma16x4(va, ds[t][jt][r], at[t][dt]);
+              const float vta =
+                  (D % 16 == 0 || col < D) ? Vts[t * Sh::kTileFloats + row * LD + col] : 0.f;
+              ct[t][dt] = mfma16x4(vta, sc[jt][r], ct[t][dt]);
+            }
           }
         }
+      }
+      __builtin_amdgcn_sched_barrier(0);
+    }
+  }
+
+  if (active) {
+    float inv = 1.f;
+    float l2tot = 0.f;
+    if constexpr (!GIVEN_LSE) {
+      l2tot = group_sum(lsum);
+      inv = 1.f / l2tot;
+    }
+    float mut[TT];
+#pragma unroll
+    for (int t = 0; t < T; ++t) mut[t] = group_sum(mu[t]) * inv;
+    if (qvalid) {
+      const int64_t obase = bnhd(b, qsite, h, N, H, D);
+#pragma unroll
+      for (int dt = 0; dt < DT; ++dt) {
+        const int d0 = dt * 16 + 4 * g;
+        if (D % 16 != 0 && d0 >= D) continue;
+        float o4[4];
+        if constexpr (!GIVEN_LSE) {
+#pragma unroll
+          for (int r = 0; r < 4; ++r) o4[r] = o[dt][r] * inv;
+          store4<S>(p.out, obase + d0, o4[0], o4[1], o4[2], o4[3]);
+        } else {
+          const float4 x = load4<S>(p.out_in, obase + d0);
+          o4[0] = x.x;
+          o4[1] = x.y;
+          o4[2] = x.z;
+          o4[3] = x.w;
+        }
+#pragma unroll
+        for (int t = 0; t < T; ++t) {
+          float tv[4];
+#pragma unroll
+          for (int r = 0; r < 4; ++r) tv[r] = (at[t][dt][r] + ct[t][dt][r]) * inv - mut[t] * o4[r];
+          store4<S>(p.tout, t * p.t_stride + obase + d0, tv[0], tv[1], tv[2], tv[3]);
+        }
+      }
+      if constexpr (!GIVEN_LSE) {
+        if (g == 0 && p.lse != nullptr)
+          p.lse[(static_cast<int64_t>(b) * N + qsite) * H + h] = (m2 + log2f(l2tot)) * kLn2;
       }
     }
   }
 
-  if (!active) return;
-  float inv = 1.f;
-  float l2tot = 0.f;
-  if constexpr (!GIVEN_LSE) {
-    l2tot = group_sum(lsum);
-    inv = 1.f / l2tot;
-  }
-  float mut[T > 0 ? T : 1];
+  // Rows of masked queries (square mask only) are exact zeros; lse takes the value the
+  // reference's all -1e4 row produces, -1e4 + log(N). Decided from the LDS copy of the
+  // mask, after the compute so these stores never delay a load.
+  if (!p.key_mask) {
+    const int r0 = blk * 64;
+    for (int it = tid; it < 64 * C4; it += 256) {
+      const int r = r0 + it / C4;
+      const int c4 = it % C4;
+      if (r < N && mask_s[r] == 0) {
+        const int64_t off = bnhd(b, r, h, N, H, D) + c4 * 4;
+        if constexpr (!GIVEN_LSE) store4<S>(p.out, off, 0.f, 0.f, 0.f, 0.f);
 #pragma unroll
-  for (int t = 0; t < T; ++t) mut[t] = group_sum(mu[t]) * inv;
-  if (qsite < 0) return;
-
-  const int64_t obase = bnhd(b, qsite, h, N, H, D);
-#pragma unroll
-  for (int dt = 0; dt < DT; ++dt) {
-    const int d0 = dt * 16 + 4 * g;
-    if (D % 16 != 0 && d0 >= D) continue;
-    float o4[4];
-    if constexpr (!GIVEN_LSE) {
-#pragma unroll
-      for (int r = 0; r < 4; ++r) o4[r] = o[dt][r] * inv;
-      store4<S>(p.out, obase + d0, o4[0], o4[1], o4[2], o4[3]);
-    } else {
-      const float4 x = load4<S>(p.out_in, obase + d0);
-      o4[0] = x.x;
-      o4[1] = x.y;
-      o4[2] = x.z;
-      o4[3] = x.w;
+        for (int t = 0; t < T; ++t) store4<S>(p.tout, t * p.t_stride + off, 0.f, 0.f, 0.f, 0.f);
+        if (!GIVEN_LSE && c4 == 0 && p.lse != nullptr)
+          p.lse[(static_cast<int64_t>(b) * N + r) * H + h] = p.masked_lse;
+      }
     }
-#pragma unroll
-    for (int t = 0; t < T; ++t) {
-      float tv[4];
-#pragma unroll
-      for (int r = 0; r < 4; ++r) tv[r] = (at[t][dt][r] + ct[t][dt][r]) * inv - mut[t] * o4[r];
-      store4<S>(p.tout, t * p.t_stride + obase + d0, tv[0], tv[1], tv[2], tv[3]);
-    }
-  }
-  if constexpr (!GIVEN_LSE) {
-    if (g == 0 && p.lse != nullptr)
-      p.lse[(static_cast<int64_t>(b) * N + qsite) * H + h] = (m2 + log2f(l2tot)) * kLn2;
   }
 }
 
@@ -338,7 +417,8 @@ hipError_t launch_fwd_t(const FwdParams& p, hipStream_t stream) {
   const int nblk = (p.N + 63) / 64;
   const int64_t nwg = static_cast<int64_t>(p.B) * p.H * nblk;
   const size_t lds = FwdShape<D, T>::lds_bytes(p.N);
-  auto kern = mhsea_fwd_kernel<D, T, GIVEN_LSE, HAS_E, S>;
+  auto kern = p.N > FwdShape<D, T>::KC ? mhsea_fwd_kernel<D, T, GIVEN_LSE, HAS_E, S, true>
+                                       : mhsea_fwd_kernel<D, T, GIVEN_LSE, HAS_E, S, false>;
   if (lds > 64 * 1024) {
     hipError_t err = hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
                                          hipFuncAttributeMaxDynamicSharedMemorySize,
@@ -381,8 +461,30 @@ hipError_t dispatch_d(const FwdParams& p, int D, int T, bool given_lse, hipStrea
 
 }  // namespace
 
+hipError_t device_cu_count(int* cus) {
+  constexpr int kMaxDevices = 64;
+  static int cached[kMaxDevices] = {0};
+  int dev = 0;
+  hipError_t err = hipGetDevice(&dev);
+  if (err != hipSuccess) return err;
+  if (dev >= 0 && dev < kMaxDevices && cached[dev] > 0) {
+    *cus = cached[dev];
+    return hipSuccess;
+  }
+  int n = 0;
+  err = hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev);
+  if (err != hipSuccess) return err;
+  if (dev >= 0 && dev < kMaxDevices) cached[dev] = n;
+  *cus = n;
+  return hipSuccess;
+}
+
 hipError_t launch_fwd(const FwdParams& p, int D, int T, bool given_lse, int dtype,
                       hipStream_t stream) {
+  if (!p.force_generic) {
+    if (small_fwd_supported(p.N, D, T)) return launch_fwd_small(p, D, T, given_lse, dtype, stream);
+    if (stream_fwd_supported(p.N)) return launch_fwd_stream(p, D, T, given_lse, dtype, stream);
+  }
   if (dtype == 1) return dispatch_d<BF16>(p, D, T, given_lse, stream);
   return dispatch_d<F32>(p, D, T, given_lse, stream);
 }

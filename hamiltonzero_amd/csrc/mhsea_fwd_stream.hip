@@ -1,0 +1,492 @@
+// Persistent, software-pipelined forward / forward+tangent / tangent-only MHSEA kernel for
+// N <= 64 (every key of a (walker, head) fits one LDS chunk).
+//
+// A fixed grid of workgroups walks the (walker, head) items with a stride of gridDim.x.
+// While the matrix cores work on item i from LDS, the global loads of item i+1 (key
+// rows K, V, Kt, Vt and the query fragments Q, Qt) and the mask bytes of item i+2 are
+// already in flight, so the two dependent HBM round trips of an item (mask -> site list ->
+// rows) are hidden behind the previous item's compute instead of being paid serially.
+//
+// Mask compaction needs no LDS: with N <= 64 one wave holds the whole mask row, a ballot
+// gives the physical count and a ds_permute gives every wave the permutation "perm"
+// (lane j holds the j-th physical site for j < n_phys, then the masked sites).
+//
+// Per item the four waves each own a 16-query tile of the compacted list and use the
+// transposed orientation S^T = K Q^T, O^T += V^T P^T of the LDS-streaming kernel; the
+// softmax is exact (all keys in one chunk: max, exp, sum, no rescaling).
+#include "mhsea_device.h"
+#include "mhsea_launch.h"
+
+namespace hz {
+namespace {
+
+template <int D, int T>
+struct StreamShape {
+  static constexpr int KC = 64;      // key rows staged (N <= 64)
+  static constexpr int LD = D + 4;   // padded LDS row, floats
+  static constexpr int DG = D / 4;   // contraction values per lane group in K.Q^T
+  static constexpr int DT = (D + 15) / 16;
+  static constexpr int C4 = D / 4;
+  static constexpr int NT = 2 + 2 * T;  // K, V, Kt[T], Vt[T]
+  static constexpr int TT = T > 0 ? T : 1;
+  static constexpr int kTileFloats = KC * LD;
+  static constexpr int kItems = KC * C4;
+  static constexpr int kPerThread = (kItems + 255) / 256;
+  static constexpr size_t kLdsBytes = static_cast<size_t>(NT) * kTileFloats * 4;
+  // Registers: the prefetched next item lives beside the current one; two tangents, or
+  // D = 64 with a tangent, need two waves per SIMD to stay out of scratch.
+  static constexpr int kWavesPerEu = (T > 1 || (D == 64 && T > 0)) ? 2 : 3;
+};
+
+template <int DG, class S>
+__device__ __forceinline__ void load_frag(const void* base, int64_t off, float* dst) {
+  if constexpr (DG >= 4) {
+#pragma unroll
+    for (int s = 0; s < DG; s += 4) {
+      const float4 x = load4<S>(base, off + s);
+      dst[s] = x.x;
+      dst[s + 1] = x.y;
+      dst[s + 2] = x.z;
+      dst[s + 3] = x.w;
+    }
+  } else {
+    const float2 x = load2<S>(base, off);
+    dst[0] = x.x;
+    dst[1] = x.y;
+  }
+}
+
+__device__ __forceinline__ void put4(float* dst, float4 x, bool keep) {
+  *reinterpret_cast<float4*>(dst) =
+      make_float4(keep ? x.x : 0.f, keep ? x.y : 0.f, keep ? x.z : 0.f, keep ? x.w : 0.f);
+}
+
+// Walker / head of item `it` (items are ordered walker-major).
+__device__ __forceinline__ void item_bh(int64_t it, int H, int& b, int& h) {
+  b = static_cast<int>(it / H);
+  h = static_cast<int>(it % H);
+}
+
+// Compacted-site bookkeeping of one item, lane-resident: the permutation (lane j holds
+// the j-th physical site, then the masked ones) and the physical count. Key and query
+// lists derive from it: under the square mask both are the physical sites; under the key
+// mask the queries are all sites, and so are the keys if no site is physical.
+struct Sites {
+  int perm;
+  int n_phys;
+  __device__ __forceinline__ bool key_all(bool key_mask) const { return key_mask && n_phys == 0; }
+  __device__ __forceinline__ int nk(bool key_mask, int N) const { return key_all(key_mask) ? N : n_phys; }
+  __device__ __forceinline__ int nq(bool key_mask, int N) const { return key_mask ? N : n_phys; }
+  __device__ __forceinline__ int kperm(bool key_mask) const {
+    return key_all(key_mask) ? static_cast<int>(threadIdx.x & 63) : perm;
+  }
+  __device__ __forceinline__ int qperm(bool key_mask) const {
+    return key_mask ? static_cast<int>(threadIdx.x & 63) : perm;
+  }
+};
+
+__device__ __forceinline__ Sites make_sites(uint32_t mbyte, int N) {
+  const int lane = threadIdx.x & 63;
+  const bool on = lane < N && mbyte != 0;
+  const uint64_t bal = __ballot(on);
+  Sites st;
+  st.n_phys = __popcll(bal);
+  const int below = __popcll(bal & ((uint64_t(1) << lane) - 1));
+  const int pos = on ? below : (lane < N ? st.n_phys + (lane - below) : lane);
+  st.perm = __builtin_amdgcn_ds_permute(pos << 2, lane);
+  return st;
+}
+
+template <int D, int T, bool GIVEN_LSE, bool HAS_E, class S>
+__global__ void __launch_bounds__(256, (StreamShape<D, T>::kWavesPerEu))
+    mhsea_fwd_stream_kernel(const FwdParams p) {
+  using Sh = StreamShape<D, T>;
+  constexpr int LD = Sh::LD, DG = Sh::DG, DT = Sh::DT, C4 = Sh::C4, TT = Sh::TT;
+  constexpr int NPT = Sh::kPerThread;
+  constexpr int NJT = 4;  // 16-key tiles of the 64-row chunk
+
+  extern __shared__ float4 smem4[];
+  float* const Ks = reinterpret_cast<float*>(smem4);
+  float* const Vs = Ks + Sh::kTileFloats;
+  float* const Kts = Vs + Sh::kTileFloats;
+  float* const Vts = Kts + T * Sh::kTileFloats;
+
+  const int N = p.N, H = p.H;
+  const int64_t nitems = static_cast<int64_t>(p.B) * H;
+  const int64_t stride = gridDim.x;
+  int64_t item = blockIdx.x;
+  if (item >= nitems) return;  // workgroup-uniform
+
+  const int tid = threadIdx.x;
+  const int wave = tid >> 6;
+  const int lane = tid & 63;
+  const int g = lane >> 4;
+  const int c = lane & 15;
+
+  // A null tangent pointer is replaced by its primal (always readable); the values are
+  // discarded after loading.
+  const bool has_kt = p.kt != nullptr, has_vt = p.vt != nullptr, has_qt = p.qt != nullptr;
+  const void* const ktp = has_kt ? p.kt : p.k;
+  const void* const vtp = has_vt ? p.vt : p.v;
+  const void* const qtp = has_qt ? p.qt : p.q;
+  const int64_t kts = has_kt ? p.t_stride : 0, vts = has_vt ? p.t_stride : 0;
+  const int64_t qts = has_qt ? p.t_stride : 0;
+
+  // ---- loads of one item ------------------------------------------------------------
+  float4 ck[NPT], cv[NPT], ckt[TT][NPT], cvt[TT][NPT];
+  float qn[DG], qtn[TT][DG];  // next item's query fragments
+  float lse2n = 0.f;
+
+  const bool km = p.key_mask != 0;
+  auto issue_item_loads = [&](int b, int h, const Sites& st) {
+    const int kperm = st.kperm(km), nk = st.nk(km, N);
+#pragma unroll
+    for (int u = 0; u < NPT; ++u) {
+      const int it = tid + u * 256;
+      const int r = it / C4;
+      const int sj = __shfl(kperm, r & 63, 64);
+      const bool ok = (Sh::kItems % 256 == 0 || it < Sh::kItems) && r < nk;
+      const int64_t off = bnhd(b, ok ? sj : 0, h, N, H, D) + (it % C4) * 4;
+      ck[u] = load4<S>(p.k, off);
+      cv[u] = load4<S>(p.v, off);
+#pragma unroll
+      for (int t = 0; t < T; ++t) {
+        ckt[t][u] = load4<S>(ktp, t * kts + off);
+        cvt[t][u] = load4<S>(vtp, t * vts + off);
+      }
+    }
+    const int jq = wave * 16 + c;
+    const int sq = __shfl(st.qperm(km), jq & 63, 64);
+    const int qload = jq < st.nq(km, N) ? sq : 0;
+    const int64_t qoff = bnhd(b, qload, h, N, H, D) + g * DG;
+    load_frag<DG, S>(p.q, qoff, qn);
+#pragma unroll
+    for (int t = 0; t < T; ++t) load_frag<DG, S>(qtp, t * qts + qoff, qtn[t]);
+    if constexpr (GIVEN_LSE) lse2n = p.lse_in[(static_cast<int64_t>(b) * N + qload) * H + h];
+  };
+
+  auto load_mask_byte = [&](int b) -> uint32_t {
+    return lane < N ? static_cast<uint32_t>(p.mask[static_cast<int64_t>(b) * N + lane]) : 0u;
+  };
+
+  // ---- prologue: item 0 loads in flight, item 1 mask in flight -------------------------
+  int b, h;
+  item_bh(item, H, b, h);
+  Sites cur = make_sites(load_mask_byte(b), N);
+  issue_item_loads(b, h, cur);
+  int64_t nxt = item + stride;
+  uint32_t mnext = 0;
+  if (nxt < nitems) {
+    int bn, hn;
+    item_bh(nxt, H, bn, hn);
+    mnext = load_mask_byte(bn);
+  }
+
+  while (true) {
+    // ---- stage the current item's keys; take its query fragments -----------------------
+    {
+#pragma unroll
+      for (int u = 0; u < NPT; ++u) {
+        const int it = tid + u * 256;
+        if (Sh::kItems % 256 == 0 || it < Sh::kItems) {
+          const int r = it / C4;
+          const bool ok = r < cur.nk(km, N);
+          const int so = r * LD + (it % C4) * 4;
+          put4(Ks + so, ck[u], ok);
+          put4(Vs + so, cv[u], ok);
+#pragma unroll
+          for (int t = 0; t < T; ++t) {
+            put4(Kts + t * Sh::kTileFloats + so, ckt[t][u], ok && has_kt);
+            put4(Vts + t * Sh::kTileFloats + so, cvt[t][u], ok && has_vt);
+          }
+        }
+      }
+    }
+    const int jq = wave * 16 + c;
+    const bool qvalid = jq < cur.nq(km, N);
+    const int qs_ = __shfl(cur.qperm(km), jq & 63, 64);
+    const int qsite = qvalid ? qs_ : -1;
+    const float qscale = qvalid ? p.scale : 0.f;
+    const float qtscale = has_qt ? qscale : 0.f;
+    float qf[DG], qtf[TT][DG];
+#pragma unroll
+    for (int s = 0; s < DG; ++s) {
+      qf[s] = qn[s] * qscale;
+#pragma unroll
+      for (int t = 0; t < T; ++t) qtf[t][s] = qtn[t][s] * qtscale;
+    }
+    const float lse2 = lse2n * kLog2e;
+    const int bc = b, hc = h;
+    const Sites sc_ = cur;
+    __syncthreads();
+
+    // ---- pipeline: next item's loads and the mask of the one after ----------------------
+    const bool more = nxt < nitems;  // workgroup-uniform
+    if (more) {
+      item_bh(nxt, H, b, h);
+      cur = make_sites(mnext, N);
+      issue_item_loads(b, h, cur);
+      const int64_t nn = nxt + stride;
+      if (nn < nitems) {
+        int bn, hn;
+        item_bh(nn, H, bn, hn);
+        mnext = load_mask_byte(bn);
+      }
+      nxt = nn;
+    }
+
+    // ---- compute the staged item ----------------------------------------------------
+    const bool active = wave * 16 < sc_.nq(km, N);  // wave-uniform
+    if (active) {
+      const int nk = sc_.nk(km, N);
+      const int njt = (nk + 15) >> 4;
+      const int64_t e_row = static_cast<int64_t>(bc) * N * N * H +
+                            static_cast<int64_t>(qsite < 0 ? 0 : qsite) * p.e_sq +
+                            static_cast<int64_t>(hc) * p.e_sh;
+      v4f sc[NJT];
+      v4f ds[TT][NJT];
+#pragma unroll
+      for (int jt = 0; jt < NJT; ++jt) {
+        sc[jt] = zero4();
+#pragma unroll
+        for (int t = 0; t < T; ++t) ds[t][jt] = zero4();
+      }
+#pragma unroll
+      for (int jt = 0; jt < NJT; ++jt) {
+        if (jt < njt) {
+          const float* krow = Ks + (jt * 16 + c) * LD + g * DG;
+#pragma unroll
+          for (int s = 0; s < DG; ++s) {
+            const float kv = krow[s];
+            sc[jt] = mfma16x4(kv, qf[s], sc[jt]);
+#pragma unroll
+            for (int t = 0; t < T; ++t) {
+              const float ktv = krow[(2 + t) * Sh::kTileFloats + s];
+              ds[t][jt] = mfma16x4(ktv, qf[s], ds[t][jt]);
+              ds[t][jt] = mfma16x4(kv, qtf[t][s], ds[t][jt]);
+            }
+          }
+        }
+        __builtin_amdgcn_sched_barrier(0);
+      }
+
+      float mx = -INFINITY;
+#pragma unroll
+      for (int jt = 0; jt < NJT; ++jt) {
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int j = jt * 16 + 4 * g + r;
+          const bool valid = jt < njt && j < nk;
+          float sv = sc[jt][r];
+          if constexpr (HAS_E) {
+            const int ks = __shfl(sc_.kperm(km), j & 63, 64);
+            if (valid && qsite >= 0) {
+              const int64_t eo = e_row + static_cast<int64_t>(ks) * p.e_sk;
+              if (p.e != nullptr) sv += load1<S>(p.e, eo);
+              if (p.et != nullptr) {
+#pragma unroll
+                for (int t = 0; t < T; ++t) ds[t][jt][r] += load1<S>(p.et, t * p.et_stride + eo);
+              }
+            }
+          }
+          sc[jt][r] = valid ? sv * kLog2e : -INFINITY;
+#pragma unroll
+          for (int t = 0; t < T; ++t) ds[t][jt][r] = valid ? ds[t][jt][r] : 0.f;
+          mx = fmaxf(mx, sc[jt][r]);
+        }
+      }
+
+      float lsum = 0.f;
+      if constexpr (GIVEN_LSE) {
+#pragma unroll
+        for (int jt = 0; jt < NJT; ++jt)
+#pragma unroll
+          for (int r = 0; r < 4; ++r) sc[jt][r] = fast_exp2(sc[jt][r] - lse2);
+      } else {
+        mx = group_max(mx);
+#pragma unroll
+        for (int jt = 0; jt < NJT; ++jt)
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            sc[jt][r] = fast_exp2(sc[jt][r] - mx);
+            lsum += sc[jt][r];
+          }
+      }
+      float mu[TT];
+#pragma unroll
+      for (int t = 0; t < T; ++t) {
+        mu[t] = 0.f;
+#pragma unroll
+        for (int jt = 0; jt < NJT; ++jt) {
+          ds[t][jt] *= sc[jt];
+          mu[t] += (ds[t][jt][0] + ds[t][jt][1]) + (ds[t][jt][2] + ds[t][jt][3]);
+        }
+      }
+
+      v4f o[DT];
+      v4f at[TT][DT];
+      v4f ct[TT][DT];
+#pragma unroll
+      for (int dt = 0; dt < DT; ++dt) {
+        o[dt] = zero4();
+#pragma unroll
+        for (int t = 0; t < T; ++t) at[t][dt] = ct[t][dt] = zero4();
+      }
+#pragma unroll
+      for (int jt = 0; jt < NJT; ++jt) {
+        if (jt < njt) {
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            const int row = jt * 16 + 4 * g + r;
+#pragma unroll
+            for (int dt = 0; dt < DT; ++dt) {
+              const int col = dt * 16 + c;
+              const float va = (D % 16 == 0 || col < D) ? Vs[row * LD + col] : 0.f;
+              if constexpr (!GIVEN_LSE) o[dt] = mfma16x4(va, sc[jt][r], o[dt]);
+#pragma unroll
+              for (int t = 0; t < T; ++t) {
+                at[t][dt] = mfma16x4(va, ds[t][jt][r], at[t][dt]);
+                const float vta =
+                    (D % 16 == 0 || col < D) ? Vts[t * Sh::kTileFloats + row * LD + col] : 0.f;
+                ct[t][dt] = mfma16x4(vta, sc[jt][r], ct[t][dt]);
+              }
+            }
+          }
+        }
+        __builtin_amdgcn_sched_barrier(0);
+      }
+
+      float inv = 1.f, ltot = 0.f;
+      if constexpr (!GIVEN_LSE) {
+        ltot = group_sum(lsum);
+        inv = 1.f / ltot;
+      }
+      float mut[TT];
+#pragma unroll
+      for (int t = 0; t < T; ++t) mut[t] = group_sum(mu[t]) * inv;
+      if (qsite >= 0) {
+        const int64_t obase = bnhd(bc, qsite, hc, N, H, D);
+#pragma unroll
+        for (int dt = 0; dt < DT; ++dt) {
+          const int d0 = dt * 16 + 4 * g;
+          if (D % 16 != 0 && d0 >= D) continue;
+          float o4[4];
+          if constexpr (!GIVEN_LSE) {
+#pragma unroll
+            for (int r = 0; r < 4; ++r) o4[r] = o[dt][r] * inv;
+            store4<S>(p.out, obase + d0, o4[0], o4[1], o4[2], o4[3]);
+          } else {
+            const float4 x = load4<S>(p.out_in, obase + d0);
+            o4[0] = x.x;
+            o4[1] = x.y;
+            o4[2] = x.z;
+            o4[3] = x.w;
+          }
+#pragma unroll
+          for (int t = 0; t < T; ++t) {
+            float tv[4];
+#pragma unroll
+            for (int r = 0; r < 4; ++r) tv[r] = (at[t][dt][r] + ct[t][dt][r]) * inv - mut[t] * o4[r];
+            store4<S>(p.tout, t * p.t_stride + obase + d0, tv[0], tv[1], tv[2], tv[3]);
+          }
+        }
+        if constexpr (!GIVEN_LSE) {
+          if (g == 0 && p.lse != nullptr)
+            p.lse[(static_cast<int64_t>(bc) * N + qsite) * H + hc] = (mx + log2f(ltot)) * kLn2;
+        }
+      }
+    }
+
+    // ---- rows of masked queries (square mask): exact zeros, lse = -1e4 + log N ---------
+    if (!p.key_mask) {
+      const int nmask = N - sc_.n_phys;
+      for (int base = 0; base < nmask * C4; base += 256) {
+        const int it = base + tid;
+        const int site = __shfl(sc_.perm, (sc_.n_phys + it / C4) & 63, 64);
+        if (it < nmask * C4) {
+          const int64_t off = bnhd(bc, site, hc, N, H, D) + (it % C4) * 4;
+          if constexpr (!GIVEN_LSE) store4<S>(p.out, off, 0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+          for (int t = 0; t < T; ++t) store4<S>(p.tout, t * p.t_stride + off, 0.f, 0.f, 0.f, 0.f);
+          if (!GIVEN_LSE && it % C4 == 0 && p.lse != nullptr)
+            p.lse[(static_cast<int64_t>(bc) * N + site) * H + hc] = p.masked_lse;
+        }
+      }
+    }
+
+    if (!more) break;
+    __syncthreads();  // every wave is done with this item's LDS tiles
+  }
+}
+
+template <int D, int T, bool GIVEN_LSE, bool HAS_E, class S>
+hipError_t launch_stream_t(const FwdParams& p, hipStream_t stream) {
+  using Sh = StreamShape<D, T>;
+  auto kern = mhsea_fwd_stream_kernel<D, T, GIVEN_LSE, HAS_E, S>;
+  const size_t lds = Sh::kLdsBytes;
+  if (lds > 64 * 1024) {
+    hipError_t err = hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
+                                         hipFuncAttributeMaxDynamicSharedMemorySize,
+                                         static_cast<int>(lds));
+    if (err != hipSuccess) return err;
+  }
+  // Enough workgroups to fill every CU at the occupancy the kernel's resources allow
+  // (queried once per kernel; the CU count once per device).
+  static int per_cu = 0;
+  if (per_cu == 0) {
+    int n = 0;
+    hipError_t err = hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, reinterpret_cast<const void*>(kern), 256, lds);
+    if (err != hipSuccess) return err;
+    per_cu = n > 0 ? n : 1;
+  }
+  int cus = 0;
+  hipError_t err = device_cu_count(&cus);
+  if (err != hipSuccess) return err;
+  const int64_t nitems = static_cast<int64_t>(p.B) * p.H;
+  int64_t grid = static_cast<int64_t>(cus) * per_cu;
+  if (grid > nitems) grid = nitems;
+  hipLaunchKernelGGL(kern, dim3(static_cast<unsigned>(grid)), dim3(256), lds, stream, p);
+  return hipGetLastError();
+}
+
+template <int D, int T, bool GIVEN_LSE, class S>
+hipError_t dispatch_e(const FwdParams& p, hipStream_t stream) {
+  if (p.e != nullptr || p.et != nullptr) return launch_stream_t<D, T, GIVEN_LSE, true, S>(p, stream);
+  return launch_stream_t<D, T, GIVEN_LSE, false, S>(p, stream);
+}
+
+template <int D, class S>
+hipError_t dispatch_t(const FwdParams& p, int T, bool given_lse, hipStream_t stream) {
+  if (given_lse) {
+    if (T == 1) return dispatch_e<D, 1, true, S>(p, stream);
+    if (T == 2) return dispatch_e<D, 2, true, S>(p, stream);
+    return hipErrorInvalidValue;
+  }
+  if (T == 0) return dispatch_e<D, 0, false, S>(p, stream);
+  if (T == 1) return dispatch_e<D, 1, false, S>(p, stream);
+  if (T == 2) return dispatch_e<D, 2, false, S>(p, stream);
+  return hipErrorInvalidValue;
+}
+
+template <class S>
+hipError_t dispatch_d(const FwdParams& p, int D, int T, bool given_lse, hipStream_t stream) {
+  switch (D) {
+    case 8: return dispatch_t<8, S>(p, T, given_lse, stream);
+    case 16: return dispatch_t<16, S>(p, T, given_lse, stream);
+    case 32: return dispatch_t<32, S>(p, T, given_lse, stream);
+    case 64: return dispatch_t<64, S>(p, T, given_lse, stream);
+    default: return hipErrorInvalidValue;
+  }
+}
+
+}  // namespace
+
+bool stream_fwd_supported(int N) { return N <= 64; }
+
+hipError_t launch_fwd_stream(const FwdParams& p, int D, int T, bool given_lse, int dtype,
+                             hipStream_t stream) {
+  if (dtype == 1) return dispatch_d<BF16>(p, D, T, given_lse, stream);
+  return dispatch_d<F32>(p, D, T, given_lse, stream);
+}
+
+}  // namespace hz

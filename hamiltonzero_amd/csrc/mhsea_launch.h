@@ -29,6 +29,7 @@ struct FwdParams {
   float scale;
   int key_mask;  // 1: reference_edge_attention masking (keys only)
   float masked_lse;
+  int force_generic;  // 1: always use the LDS-streaming kernel
 };
 
 struct BwdParams {
@@ -56,5 +57,26 @@ hipError_t launch_fwd(const FwdParams& p, int D, int T, bool given_lse, int dtyp
                       hipStream_t stream);
 
 hipError_t launch_bwd(const BwdParams& p, int D, int dtype, hipStream_t stream);
+
+// Register-resident kernel for N <= 64: a wave keeps every key operand of its
+// (walker, head) in registers, K/Kt as D/4 and V/Vt as 4 ceil(D/16) floats per key tile
+// and tensor; the budget of 128 such floats bounds the number of 16-key tiles.
+constexpr int small_max_key_tiles(int D, int T) {
+  return (128 / ((D / 4 + 4 * ((D + 15) / 16)) * (1 + T))) > 4
+             ? 4
+             : (128 / ((D / 4 + 4 * ((D + 15) / 16)) * (1 + T)));
+}
+template <int D, int T>
+struct SmallFits {
+  static constexpr int kMaxKeyTiles = small_max_key_tiles(D, T);
+};
+bool small_fwd_supported(int N, int D, int T);
+bool stream_fwd_supported(int N);
+hipError_t launch_fwd_stream(const FwdParams& p, int D, int T, bool given_lse, int dtype,
+                             hipStream_t stream);
+// Compute units of the current device (cached per device).
+hipError_t device_cu_count(int* cus);
+hipError_t launch_fwd_small(const FwdParams& p, int D, int T, bool given_lse, int dtype,
+                            hipStream_t stream);
 
 }  // namespace hz

@@ -9,6 +9,9 @@ Layouts follow the reference primitives (``_pallas_attn/utils.py:21-36``):
 ``q, k, v: [B, N, H, D]``, ``e: [B, N, H, N]`` (or ``[B, N, N, H]`` with
 ``e_layout="qkh"``), ``mask: [B, N]`` bool, ``lse: [B, N, H]`` float32, tangents
 ``[T, B, N, H, D]`` or a single ``[B, N, H, D]`` direction.
+
+Every call takes ``generic=True`` to force the LDS-streaming kernels (``HZ_FLAG_GENERIC``)
+instead of the automatic choice, for testing and comparison.
 """
 
 from __future__ import annotations
@@ -33,11 +36,13 @@ def _stream(device: torch.device) -> int:
     return torch.cuda.current_stream(device).cuda_stream
 
 
-def _flags(key_mask: bool, e_layout: str) -> int:
+def _flags(key_mask: bool, e_layout: str, generic: bool = False) -> int:
     if e_layout not in ("qhk", "qkh"):
         raise ValueError(f"e_layout must be 'qhk' or 'qkh', got {e_layout!r}")
-    return (_native.HZ_FLAG_KEY_MASK if key_mask else 0) | (
-        _native.HZ_FLAG_E_QKH if e_layout == "qkh" else 0
+    return (
+        (_native.HZ_FLAG_KEY_MASK if key_mask else 0)
+        | (_native.HZ_FLAG_E_QKH if e_layout == "qkh" else 0)
+        | (_native.HZ_FLAG_GENERIC if generic else 0)
     )
 
 
@@ -116,6 +121,7 @@ def mhsea_fwd(
     scale: float = 1.0,
     key_mask: bool = False,
     e_layout: str = "qhk",
+    generic: bool = False,
     with_lse: bool = True,
 ) -> Tuple[Tensor, Optional[Tensor]]:
     """Forward: returns ``(out, lse)`` (lse is None when ``with_lse`` is False)."""
@@ -127,7 +133,7 @@ def mhsea_fwd(
     _native.check(
         _native.lib().hz_mhsea_fwd(
             _stream(q.device), _ptr(q), _ptr(k), _ptr(e), _ptr(v), _ptr(m), _ptr(out), _ptr(lse),
-            B, N, H, D, _DTYPES[q.dtype], float(scale), _flags(key_mask, e_layout),
+            B, N, H, D, _DTYPES[q.dtype], float(scale), _flags(key_mask, e_layout, generic),
         )
     )
     return out, lse
@@ -149,6 +155,7 @@ def mhsea_jvp(
     scale: float = 1.0,
     key_mask: bool = False,
     e_layout: str = "qhk",
+    generic: bool = False,
 ) -> Tensor:
     """Tangent of the forward given its primal ``(out, lse)`` (the reference's lin primitive).
 
@@ -170,7 +177,7 @@ def mhsea_jvp(
         _native.lib().hz_mhsea_jvp(
             _stream(q.device), _ptr(q), _ptr(k), _ptr(e), _ptr(v), _ptr(m), _ptr(out), _ptr(lse),
             _ptr(qt), _ptr(kt), _ptr(et), _ptr(vt), T, _ptr(tout),
-            B, N, H, D, _DTYPES[q.dtype], float(scale), _flags(key_mask, e_layout),
+            B, N, H, D, _DTYPES[q.dtype], float(scale), _flags(key_mask, e_layout, generic),
         )
     )
     return tout if batched else tout[0]
@@ -190,6 +197,7 @@ def mhsea_fwd_jvp(
     scale: float = 1.0,
     key_mask: bool = False,
     e_layout: str = "qhk",
+    generic: bool = False,
     with_lse: bool = True,
 ) -> Tuple[Tensor, Optional[Tensor], Tensor]:
     """Fused forward + tangents: returns ``(out, lse, tout)`` in one pass over K/V."""
@@ -206,7 +214,7 @@ def mhsea_fwd_jvp(
         _native.lib().hz_mhsea_fwd_jvp(
             _stream(q.device), _ptr(q), _ptr(k), _ptr(e), _ptr(v), _ptr(m),
             _ptr(qt), _ptr(kt), _ptr(et), _ptr(vt), T, _ptr(out), _ptr(lse), _ptr(tout),
-            B, N, H, D, _DTYPES[q.dtype], float(scale), _flags(key_mask, e_layout),
+            B, N, H, D, _DTYPES[q.dtype], float(scale), _flags(key_mask, e_layout, generic),
         )
     )
     return out, lse, (tout if batched else tout[0])
@@ -226,6 +234,7 @@ def mhsea_bwd(
     scale: float = 1.0,
     key_mask: bool = False,
     e_layout: str = "qhk",
+    generic: bool = False,
 ) -> Tuple[Tensor, Tensor, Optional[Tensor], Tensor]:
     """Reverse mode: returns ``(dq, dk, de, dv)`` (de is None when not requested)."""
     B, N, H, D = _check_primals(q, k, v, mask, e, e_layout)
@@ -245,7 +254,7 @@ def mhsea_bwd(
         _native.lib().hz_mhsea_bwd(
             _stream(q.device), _ptr(q), _ptr(k), _ptr(e), _ptr(v), _ptr(m), _ptr(lse), _ptr(out),
             _ptr(dout), _ptr(dq), _ptr(dk), _ptr(de), _ptr(dv),
-            B, N, H, D, _DTYPES[q.dtype], float(scale), _flags(key_mask, e_layout),
+            B, N, H, D, _DTYPES[q.dtype], float(scale), _flags(key_mask, e_layout, generic),
         )
     )
     return dq, dk, de, dv

@@ -67,7 +67,8 @@ enum hz_dtype { HZ_DTYPE_F32 = 0, HZ_DTYPE_BF16 = 1 };
 
 enum hz_flags {
   HZ_FLAG_KEY_MASK = 1, /* reference_edge_attention masking instead of the square mask */
-  HZ_FLAG_E_QKH = 2     /* e / et / de are [B, N(query), N(key), H] */
+  HZ_FLAG_E_QKH = 2,    /* e / et / de are [B, N(query), N(key), H] */
+  HZ_FLAG_GENERIC = 4   /* always use the LDS-streaming kernels (testing / comparison) */
 };
 
 enum hz_status {

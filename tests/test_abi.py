@@ -55,7 +55,7 @@ def _fwd(lib, **over):
         (dict(N=_native.HZ_MAX_N + 1), _native.HZ_EINVAL, "N must be"),
         (dict(B=0), _native.HZ_EINVAL, "B and H"),
         (dict(dtype=7), _native.HZ_EINVAL, "dtype"),
-        (dict(flags=8), _native.HZ_EINVAL, "flag"),
+        (dict(flags=16), _native.HZ_EINVAL, "flag"),
         (dict(q=None), _native.HZ_ENULL, "q must not be NULL"),
         (dict(mask=None), _native.HZ_ENULL, "mask"),
         (dict(out=None), _native.HZ_ENULL, "out"),

@@ -101,7 +101,11 @@ CASES = [
 IDS = [c[0] for c in CASES]
 
 
-def _setup(case):
+PATHS = [False, True]
+PATH_IDS = ["auto", "generic"]
+
+
+def _setup(case, generic=False):
     name, B, N, H, D, n_phys, scattered, with_e, e_layout, key_mask, scale, T, bf16 = case
     a = make_inputs(zlib.crc32(name.encode()) % 1000, B, N, H, D, n_phys, scattered=scattered, with_e=with_e,
                     e_layout=e_layout, T=T, bf16=bf16)
@@ -109,16 +113,17 @@ def _setup(case):
     d = {n: to_dev(x, dt) for n, x in a.items()}
     opts = dict(scale=scale, key_mask=key_mask, e_layout=e_layout)
     tol = BF16_TOL if bf16 else F32_TOL
-    return a, d, opts, tol, T
+    return a, d, opts, dict(opts, generic=generic), tol, T
 
 
+@pytest.mark.parametrize("generic", PATHS, ids=PATH_IDS)
 @pytest.mark.parametrize("case", CASES, ids=IDS)
-def test_fwd_parity(case):
+def test_fwd_parity(case, generic):
     from hamiltonzero_amd import kernels
 
-    _say(f"fwd {case[0]}")
-    a, d, opts, tol, _ = _setup(case)
-    out, lse = kernels.mhsea_fwd(d["q"], d["k"], d["v"], d["mask"], d["e"], **opts)
+    _say(f"fwd {case[0]} generic={generic}")
+    a, d, opts, kopts, tol, _ = _setup(case, generic)
+    out, lse = kernels.mhsea_fwd(d["q"], d["k"], d["v"], d["mask"], d["e"], **kopts)
     torch.cuda.synchronize()
     ref_out, ref_lse = O.fwd(a["q"], a["k"], a["e"], a["v"], a["mask"], **opts)
     assert rel(host(out), ref_out) <= tol
@@ -134,14 +139,15 @@ def test_fwd_parity(case):
             assert rel(host(lse)[sel], ref_lse[sel]) <= tol
 
 
+@pytest.mark.parametrize("generic", PATHS, ids=PATH_IDS)
 @pytest.mark.parametrize("case", CASES, ids=IDS)
-def test_fwd_jvp_parity(case):
+def test_fwd_jvp_parity(case, generic):
     from hamiltonzero_amd import kernels
 
-    _say(f"fwd_jvp {case[0]}")
-    a, d, opts, tol, T = _setup(case)
+    _say(f"fwd_jvp {case[0]} generic={generic}")
+    a, d, opts, kopts, tol, T = _setup(case, generic)
     out, lse, tout = kernels.mhsea_fwd_jvp(d["q"], d["k"], d["v"], d["mask"], d["qt"], d["kt"], d["vt"],
-                                           d["e"], d["et"], **opts)
+                                           d["e"], d["et"], **kopts)
     torch.cuda.synchronize()
     ref_out, _ = O.fwd(a["q"], a["k"], a["e"], a["v"], a["mask"], **opts)
     assert rel(host(out), ref_out) <= tol
@@ -154,15 +160,16 @@ def test_fwd_jvp_parity(case):
             assert np.all(got[~a["mask"]] == 0.0)
 
 
+@pytest.mark.parametrize("generic", PATHS, ids=PATH_IDS)
 @pytest.mark.parametrize("case", CASES, ids=IDS)
-def test_jvp_given_lse_parity(case):
+def test_jvp_given_lse_parity(case, generic):
     from hamiltonzero_amd import kernels
 
-    _say(f"jvp {case[0]}")
-    a, d, opts, tol, T = _setup(case)
-    out, lse = kernels.mhsea_fwd(d["q"], d["k"], d["v"], d["mask"], d["e"], **opts)
+    _say(f"jvp {case[0]} generic={generic}")
+    a, d, opts, kopts, tol, T = _setup(case, generic)
+    out, lse = kernels.mhsea_fwd(d["q"], d["k"], d["v"], d["mask"], d["e"], **kopts)
     tout = kernels.mhsea_jvp(d["q"], d["k"], d["v"], d["mask"], out, lse, d["qt"], d["kt"], d["vt"],
-                             d["e"], d["et"], **opts)
+                             d["e"], d["et"], **kopts)
     torch.cuda.synchronize()
     for t in range(T):
         et = None if a["et"] is None else a["et"][t]
@@ -175,10 +182,10 @@ def test_bwd_parity(case):
     from hamiltonzero_amd import kernels
 
     _say(f"bwd {case[0]}")
-    a, d, opts, tol, _ = _setup(case)
-    out, lse = kernels.mhsea_fwd(d["q"], d["k"], d["v"], d["mask"], d["e"], **opts)
+    a, d, opts, kopts, tol, _ = _setup(case)
+    out, lse = kernels.mhsea_fwd(d["q"], d["k"], d["v"], d["mask"], d["e"], **kopts)
     dq, dk, de, dv = kernels.mhsea_bwd(d["q"], d["k"], d["v"], d["mask"], lse, out, d["dout"], d["e"],
-                                       want_de=True, **opts)
+                                       want_de=True, **kopts)
     torch.cuda.synchronize()
     ref = O.vjp(a["q"], a["k"], a["e"], a["v"], a["mask"], a["dout"], **opts)
     floors = vjp_floors(a, opts)
