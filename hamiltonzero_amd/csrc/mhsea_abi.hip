@@ -245,6 +245,7 @@ int hz_mhsea_bwd(hipStream_t stream, const void* q, const void* k, const void* e
   set_e_strides(N, H, flags, p.e_sq, p.e_sh, p.e_sk);
   p.scale = scale;
   p.key_mask = (flags & HZ_FLAG_KEY_MASK) ? 1 : 0;
+  p.force_generic = (flags & HZ_FLAG_GENERIC) ? 1 : 0;
   return launched(hz::launch_bwd(p, static_cast<int>(D), dtype, stream));
 }
 

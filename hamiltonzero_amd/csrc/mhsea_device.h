@@ -37,11 +37,14 @@ __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_ex
 __device__ __forceinline__ float bf16_to_f32(uint16_t x) {
   return __uint_as_float(static_cast<uint32_t>(x) << 16);
 }
+// Hardware conversion (v_cvt_pk_bf16_f32 on gfx950): round to nearest even, NaN stays NaN.
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+typedef float f32x2_t __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ uint32_t pack2_bf16(float lo, float hi) {
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2_t{lo, hi}), bf16x2_t));
+}
 __device__ __forceinline__ uint16_t f32_to_bf16(float f) {
-  uint32_t u = __float_as_uint(f);
-  if ((u & 0x7fffffffu) > 0x7f800000u) return static_cast<uint16_t>((u >> 16) | 0x40u);
-  u += 0x7fffu + ((u >> 16) & 1u);
-  return static_cast<uint16_t>(u >> 16);
+  return static_cast<uint16_t>(pack2_bf16(f, 0.f) & 0xffffu);
 }
 
 // Storage policy: F32 tensors are float, BF16 tensors are uint16_t bit patterns.
@@ -67,6 +70,30 @@ __device__ __forceinline__ float4 load4<BF16>(const void* base, int64_t off) {
   return make_float4(__uint_as_float(u.x << 16), __uint_as_float(u.x & 0xffff0000u),
                      __uint_as_float(u.y << 16), __uint_as_float(u.y & 0xffff0000u));
 }
+
+// Four consecutive elements in their storage format, for values that are loaded early and
+// used late (prefetch registers): bfloat16 keeps half the registers of float.
+template <class S>
+struct Raw4;
+template <>
+struct Raw4<F32> {
+  float4 v;
+  __device__ __forceinline__ static Raw4 load(const void* base, int64_t off) {
+    return Raw4{*reinterpret_cast<const float4*>(static_cast<const float*>(base) + off)};
+  }
+  __device__ __forceinline__ float4 f() const { return v; }
+};
+template <>
+struct Raw4<BF16> {
+  uint2 v;
+  __device__ __forceinline__ static Raw4 load(const void* base, int64_t off) {
+    return Raw4{*reinterpret_cast<const uint2*>(static_cast<const uint16_t*>(base) + off)};
+  }
+  __device__ __forceinline__ float4 f() const {
+    return make_float4(__uint_as_float(v.x << 16), __uint_as_float(v.x & 0xffff0000u),
+                       __uint_as_float(v.y << 16), __uint_as_float(v.y & 0xffff0000u));
+  }
+};
 
 // Load 2 consecutive elements (8 B aligned for F32, 4 B for BF16) as float.
 template <class S>
@@ -104,8 +131,8 @@ template <>
 __device__ __forceinline__ void store4<BF16>(void* base, int64_t off, float a, float b,
                                              float c, float d) {
   uint2 u;
-  u.x = static_cast<uint32_t>(f32_to_bf16(a)) | (static_cast<uint32_t>(f32_to_bf16(b)) << 16);
-  u.y = static_cast<uint32_t>(f32_to_bf16(c)) | (static_cast<uint32_t>(f32_to_bf16(d)) << 16);
+  u.x = pack2_bf16(a, b);
+  u.y = pack2_bf16(c, d);
   *reinterpret_cast<uint2*>(static_cast<uint16_t*>(base) + off) = u;
 }
 

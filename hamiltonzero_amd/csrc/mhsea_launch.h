@@ -49,6 +49,7 @@ struct BwdParams {
   int64_t e_sq, e_sh, e_sk;
   float scale;
   int key_mask;
+  int force_generic;  // 1: always use the two-kernel path
 };
 
 // T = tangents in this launch (0 = forward only). given_lse selects the tangent-only
@@ -74,6 +75,10 @@ bool small_fwd_supported(int N, int D, int T);
 bool stream_fwd_supported(int N);
 hipError_t launch_fwd_stream(const FwdParams& p, int D, int T, bool given_lse, int dtype,
                              hipStream_t stream);
+bool stream_bwd_supported(int N);
+hipError_t launch_bwd_stream(const BwdParams& p, int D, int dtype, hipStream_t stream);
+bool bf16_fwd_supported(int D);
+hipError_t launch_fwd_bf16(const FwdParams& p, int D, int T, bool given_lse, hipStream_t stream);
 // Compute units of the current device (cached per device).
 hipError_t device_cu_count(int* cus);
 hipError_t launch_fwd_small(const FwdParams& p, int D, int T, bool given_lse, int dtype,

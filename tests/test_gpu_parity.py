@@ -177,12 +177,13 @@ def test_jvp_given_lse_parity(case, generic):
         assert rel(host(tout)[t], ref_t) <= tol, f"tangent {t}"
 
 
+@pytest.mark.parametrize("generic", PATHS, ids=PATH_IDS)
 @pytest.mark.parametrize("case", CASES, ids=IDS)
-def test_bwd_parity(case):
+def test_bwd_parity(case, generic):
     from hamiltonzero_amd import kernels
 
-    _say(f"bwd {case[0]}")
-    a, d, opts, kopts, tol, _ = _setup(case)
+    _say(f"bwd {case[0]} generic={generic}")
+    a, d, opts, kopts, tol, _ = _setup(case, generic)
     out, lse = kernels.mhsea_fwd(d["q"], d["k"], d["v"], d["mask"], d["e"], **kopts)
     dq, dk, de, dv = kernels.mhsea_bwd(d["q"], d["k"], d["v"], d["mask"], lse, out, d["dout"], d["e"],
                                        want_de=True, **kopts)
