@@ -94,6 +94,32 @@ def traffic_from_profile(config):
     return rec.get("traffic_bytes_per_launch")
 
 
+def copy_probe(mib, steps, warmup):
+    """Device-to-device copies of a known size (hipMemcpyAsync -> the runtime's copyBuffer
+    kernel): reads and writes exactly ``mib`` MiB per launch. Profiled under rocprofv3
+    --pmc it gives the factor between FETCH_SIZE / WRITE_SIZE and real bytes."""
+    import torch
+
+    n = mib * (1 << 20) // 4
+    src = torch.ones(n, dtype=torch.float32, device="cuda:0")
+    dst = torch.empty_like(src)
+    for _ in range(warmup):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    ev0 = torch.cuda.Event(enable_timing=True)
+    ev1 = torch.cuda.Event(enable_timing=True)
+    ev0.record()
+    for _ in range(steps):
+        dst.copy_(src)
+    ev1.record()
+    torch.cuda.synchronize()
+    ms = ev0.elapsed_time(ev1) / steps
+    nbytes = n * 4
+    print(json.dumps({"copy_probe_bytes": nbytes, "ms_per_copy": ms,
+                      "gbs_read_plus_write": 2 * nbytes / ms / 1e6}), flush=True)
+    return 0
+
+
 def main(argv=None):
     ap = argparse.ArgumentParser(description=__doc__.splitlines()[0])
     ap.add_argument("--gpus", type=int, default=1)
@@ -104,6 +130,9 @@ def main(argv=None):
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--generic", action="store_true",
                     help="force the LDS-streaming kernels (HZ_FLAG_GENERIC) for comparison")
+    ap.add_argument("--copy-probe", type=int, default=0, metavar="MIB",
+                    help="instead of a configuration, time device-to-device copies of MIB MiB "
+                         "(the calibration kernel for rocprofv3 FETCH_SIZE / WRITE_SIZE)")
     args = ap.parse_args(argv)
 
     if args.gpus != 1:
@@ -114,6 +143,9 @@ def main(argv=None):
     import torch
 
     from hamiltonzero_amd import _native
+
+    if args.copy_probe:
+        return copy_probe(args.copy_probe, args.steps, args.warmup)
 
     lib = _native.lib()
     work, B, N, H, D, n_phys, T, dtype, seed, desc = CONFIGS[args.config]

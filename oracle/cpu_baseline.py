@@ -93,7 +93,7 @@ def time_walkers_per_s(work: str, B: int, N: int, H: int, D: int, n_phys: int, s
             fn()
             reps += 1
             el = time.perf_counter() - t0
-            if el >= budget_s or reps >= 1000:
+            if el >= budget_s or reps >= 100000:
                 break
     return {
         "walkers_per_s": B * reps / el,
