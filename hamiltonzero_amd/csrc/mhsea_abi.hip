@@ -40,6 +40,8 @@ int check_dims(int64_t B, int64_t N, int64_t H, int64_t D, int dtype, int flags)
   if (flags & ~(HZ_FLAG_KEY_MASK | HZ_FLAG_E_QKH | HZ_FLAG_GENERIC)) return fail(HZ_EINVAL, "unknown flag bits 0x%x", flags);
   const int64_t nwg = B * H * ((N + 63) / 64);
   if (nwg > 0x7fffffffLL) return fail(HZ_EINVAL, "B*H*ceil(N/64) = %lld exceeds the grid limit", (long long)nwg);
+  if (B * N > 0x7fffffffLL)
+    return fail(HZ_EINVAL, "B*N = %lld exceeds the supported mask size", (long long)(B * N));
   if (B * N * H * N > (int64_t(1) << 46))
     return fail(HZ_EINVAL, "B*N*H*N = %lld exceeds the supported tensor size", (long long)(B * N * H * N));
   return HZ_OK;

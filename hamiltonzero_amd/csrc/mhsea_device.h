@@ -249,6 +249,25 @@ __device__ __forceinline__ int compact_mask_lds(const uint8_t* __restrict__ mask
   return total;
 }
 
+// Byte loads of one walker's mask row through a raw buffer resource (gfx9 descriptor,
+// dword3 = 0x00020000: 32-bit data format, no swizzle). The walker offset b*N goes into
+// the scalar offset, the lane into the vector offset. Lanes past the row (lane >= N) get
+// the vector offset num_records, which is out of range whether or not the hardware adds
+// the scalar offset before its range check, so they read 0 and never touch memory. The
+// host guarantees B*N <= 2^31 - 1, so offsets never wrap.
+struct MaskReader {
+  __amdgpu_buffer_rsrc_t rsrc;
+  int nrec;
+  __device__ __forceinline__ MaskReader(const uint8_t* mask, int64_t bytes)
+      : rsrc(__builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t*>(mask), static_cast<short>(0),
+                                               static_cast<int>(bytes), 0x00020000)),
+        nrec(static_cast<int>(bytes)) {}
+  __device__ __forceinline__ uint32_t byte(int b, int N, int lane) const {
+    const int voff = lane < N ? lane : nrec;
+    return static_cast<uint32_t>(__builtin_amdgcn_raw_buffer_load_b8(rsrc, voff, b * N, 0));
+  }
+};
+
 // Map blockIdx.x to a logical workgroup id so that consecutive logical ids (which share
 // K/V rows of one walker and head) land on the same XCD. Workgroups are dispatched to
 // the 8 XCDs round-robin by hardware id.

@@ -1,0 +1,765 @@
+// Producer/consumer forward / forward+tangent / tangent-only MHSEA kernel for float32
+// storage and N <= 64 (every key of a (walker, head) fits one LDS tile).
+//
+// A workgroup is four waves: wave 3 is the producer, waves 0-2 are consumers. A fixed grid
+// of workgroups walks the (walker, head) items; workgroup L takes items L, L+G, L+2G, ...
+// and processes them in "periods", one item per period. In period k
+//   - the consumers compute item k from LDS buffer k%2: each owns one 16-query tile of the
+//     compacted query list and runs S^T = K Q^T, the exact softmax (all keys in one tile)
+//     and O^T += V^T P^T on the fp32 matrix cores (v_mfma_f32_16x16x4_f32), with the
+//     tangent products dS^T = Kt Q^T + K Qt^T, A^T = V^T (P o dS)^T, C^T = Vt^T P^T;
+//   - the producer gathers item k+1's physical key rows (K, Kt, V, Vt) from HBM straight
+//     into LDS buffer (k+1)%2 with global_load_lds_dwordx4 (no registers hold them),
+//     zero-fills the rows of the last partial 16-key tile, writes item k+1's masked output
+//     rows (exact zeros, lse = -1e4 + log N) and reads item k+2's mask row.
+// A single s_barrier ends a period. The producer publishes each item's compacted site
+// list in one of four LDS slots two periods ahead, so the consumers can prefetch their
+// query fragments one item ahead into registers. Consumers alternate two register sets
+// (the loop is unrolled by two), so no register copy forces an early wait.
+//
+// vmcnt on gfx950 counts loads and stores together and in order: waiting for a load also
+// waits for every older memory operation. Every consumer load and store is therefore
+// unconditional — lanes without a valid row address a buffer resource past its last
+// record, which reads 0 and drops stores — so the compiler's waits are exact counts and
+// the wait for item k's query fragments never waits for item k-1's output stores. The
+// producer never computes, so its own waits (vmcnt(0) once per period) stall nobody.
+//
+// Key rows are stored unpadded (D floats per row) with the 16-byte chunks of row r XOR-
+// swizzled by (r / rows_per_128B) mod chunks_per_row, which keeps the consumers' K reads
+// (16 rows x one chunk) and V reads (4 rows x 16 floats) free of LDS bank conflicts at
+// D >= 32.
+#include "mhsea_device.h"
+#include "mhsea_launch.h"
+
+namespace hz {
+namespace {
+
+typedef __attribute__((address_space(3))) void lds_void_t;
+typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
+
+constexpr int kProducerWave = 3;
+constexpr int kSlots = 4;
+constexpr int kSlotBytes = 144;  // int16 perm[64], int32 n_phys at byte 128
+constexpr int kDmaBytes = 1024;  // one global_load_lds_dwordx4 wave instruction
+
+template <int D, int T>
+struct PcShape {
+  static constexpr int NT = 2 + 2 * T;  // K, Kt[T], V, Vt[T]
+  static constexpr int ROWB = D * 4;
+  static constexpr int CHUNKS = D / 4;  // 16-byte chunks per row
+  static constexpr int TILE = 64 * ROWB;
+  static constexpr int BUF = NT * TILE;
+  static constexpr int LDS = 2 * BUF + kSlots * kSlotBytes;
+  static constexpr int DG = D / 4;
+  static constexpr int DT = (D + 15) / 16;
+  static constexpr int TT = T > 0 ? T : 1;
+  static constexpr int C4 = D / 4;
+};
+
+// Chunk swizzle of key row r: the 16-byte chunk c of row r sits at chunk position
+// c ^ swz(r). With x = r mod 16, swz = ((x >> 2) & 3) | ((x & 1) << 2), cut to the chunks
+// of a row. It is a bijection on {x : x mod 4 in {0, 1}} and on {x : x mod 4 in {2, 3}}
+// (the rows that eight lanes of a K read touch together) and flips bit 2 between rows
+// 4m and 4m+1, 4m+2 and 4m+3 (the row pairs of a V read), so neither read pattern
+// conflicts on the 32 LDS banks for D >= 32.
+template <int D>
+__device__ __forceinline__ int swz(int r) {
+  return ((((r >> 2) & 3) | ((r & 1) << 2))) & (PcShape<D, 0>::CHUNKS - 1);
+}
+
+// Byte offset of 16-byte chunk c of key row r inside a tile.
+template <int D>
+__device__ __forceinline__ int swz_off(int r, int c) {
+  return r * PcShape<D, 0>::ROWB + ((c ^ swz<D>(r)) << 4);
+}
+
+// Inside a 16-key tile the S^T rows are a transposed 4x4 arrangement of the keys: S^T row
+// 4g + r holds key 4r + g. A lane's C-layout values r = 0..3 then hold keys 4r + g, so
+// the P.V products of contraction step r cover keys 4r..4r+3, and a partial last tile
+// (n mod 16 keys) skips the steps whose four keys are all padding.
+__device__ __forceinline__ int srow_key(int row) { return 4 * (row & 3) + (row >> 2); }
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, int64_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), static_cast<short>(0),
+                                           static_cast<int>(bytes), 0x00020000);
+}
+
+__device__ __forceinline__ void buf_store4(__amdgpu_buffer_rsrc_t r, int voff, float a, float b,
+                                           float c, float d) {
+  const u32x4_t v = {__float_as_uint(a), __float_as_uint(b), __float_as_uint(c), __float_as_uint(d)};
+  __builtin_amdgcn_raw_buffer_store_b128(v, r, voff, 0, 0);
+}
+
+__device__ __forceinline__ float buf_load1(__amdgpu_buffer_rsrc_t r, int voff) {
+  return __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(r, voff, 0, 0));
+}
+
+__device__ __forceinline__ void compiler_fence() { asm volatile("" ::: "memory"); }
+
+// s_waitcnt immediates (gfx9 encoding: vmcnt[3:0]+[15:14], expcnt[6:4], lgkmcnt[11:8]).
+constexpr int kWaitLgkm0 = 0xC07F;
+constexpr int kWaitAll0 = 0x0070;
+
+__device__ __forceinline__ void wg_barrier() {
+  compiler_fence();
+  __builtin_amdgcn_s_barrier();
+  compiler_fence();
+}
+
+// Compacted sites of one walker, lane-resident: lane j holds the j-th physical site
+// (ascending), then the masked sites (ascending).
+struct PcSites {
+  int perm;
+  int n_phys;
+};
+
+__device__ __forceinline__ PcSites pc_sites(uint32_t mbyte, int N) {
+  const int lane = threadIdx.x & 63;
+  const bool on = lane < N && mbyte != 0;
+  const uint64_t bal = __ballot(on);
+  PcSites st;
+  st.n_phys = __popcll(bal);
+  const int below = __popcll(bal & ((uint64_t(1) << lane) - 1));
+  const int pos = on ? below : (lane < N ? st.n_phys + (lane - below) : lane);
+  st.perm = __builtin_amdgcn_ds_permute(pos << 2, lane);
+  return st;
+}
+
+// Key / query lists from the site list (mask semantics of include/hz_mhsea.h): under the
+// square mask both are the physical sites; under the key mask the queries are all sites,
+// and so are the keys when no site is physical.
+__device__ __forceinline__ int pc_nk(int n_phys, bool km, int N) { return (km && n_phys == 0) ? N : n_phys; }
+__device__ __forceinline__ int pc_nq(int n_phys, bool km, int N) { return km ? N : n_phys; }
+
+struct ItemSeq {
+  uint32_t first, stride, nitems, H;
+  __device__ __forceinline__ uint32_t item(int k) const { return first + static_cast<uint32_t>(k) * stride; }
+  __device__ __forceinline__ void bh(int k, int& b, int& h) const {
+    const uint32_t it = item(k);
+    const uint32_t bq = it / H;
+    b = static_cast<int>(bq);
+    h = static_cast<int>(it - bq * H);
+  }
+};
+
+// ------------------------------------------------------------------------------------
+// Producer (wave 3)
+// ------------------------------------------------------------------------------------
+template <int D, int T, bool GIVEN_LSE>
+__device__ __forceinline__ void pc_producer(const FwdParams& p, char* lds, const ItemSeq& seq, int cnt) {
+  using Sh = PcShape<D, T>;
+  const int lane = threadIdx.x & 63;
+  const int N = p.N, H = p.H;
+  const bool km = p.key_mask != 0;
+  const MaskReader mreader(p.mask, static_cast<int64_t>(p.B) * N);
+  char* const slots = lds + 2 * Sh::BUF;
+
+  auto write_slot = [&](int k, const PcSites& st) {
+    char* s = slots + (k % kSlots) * kSlotBytes;
+    reinterpret_cast<int16_t*>(s)[lane] = static_cast<int16_t>(st.perm);
+    if (lane == 0) reinterpret_cast<int*>(s + 128)[0] = st.n_phys;
+  };
+
+  auto zero_rows = [&](char* tile, int r0, int r1) {
+    const int n = (r1 - r0) * Sh::CHUNKS;
+    for (int i = lane; i < n; i += 64) {
+      const int r = r0 + i / Sh::CHUNKS;
+      *reinterpret_cast<float4*>(tile + r * Sh::ROWB + (i % Sh::CHUNKS) * 16) = make_float4(0.f, 0.f, 0.f, 0.f);
+    }
+  };
+
+  // Item k's key tiles. The DMA lane mapping is the same for every tensor: instruction j
+  // writes tile bytes [1024 j, 1024 j + 1024), lane l the 16 bytes at 1024 j + 16 l, i.e.
+  // chunk position pch of row r_j; it reads the row's swizzled source chunk. The per-lane
+  // byte offsets inside the walker's slice are computed once per item (one batch of
+  // ds_bpermute), and each tensor then costs one global_load_lds per 1 KiB from a scalar
+  // base address. The padding rows of the last partial 16-key tile are zeroed first (no
+  // LDS-DMA is in flight to them).
+  constexpr int RPI = kDmaBytes / Sh::ROWB;  // rows per DMA instruction
+  constexpr int NJ = 64 / RPI;               // DMA instructions per full 64-row tile
+  auto fill = [&](int k, const PcSites& st) {
+    int b, h;
+    seq.bh(k, b, h);
+    char* buf = lds + (k & 1) * Sh::BUF;
+    const int nk = pc_nk(st.n_phys, km, N);
+    const int nkpad = (nk + 15) & ~15;
+    const int kperm = (km && st.n_phys == 0) ? lane : st.perm;
+    const int pch = (lane * 16 % Sh::ROWB) >> 4;
+    const int r0 = lane * 16 / Sh::ROWB;
+    uint32_t off[NJ];
+#pragma unroll
+    for (int j = 0; j < NJ; ++j) {
+      const int r = j * RPI + r0;
+      const int site = __shfl(kperm, r, 64);
+      const int c = pch ^ swz<D>(r);
+      off[j] = static_cast<uint32_t>(((site * H + h) * D) * 4 + c * 16);
+    }
+    const int nj = (nk * Sh::ROWB + kDmaBytes - 1) / kDmaBytes;
+    const int64_t wofs = static_cast<int64_t>(b) * N * H * D;  // walker offset, elements
+#pragma unroll
+    for (int x = 0; x < Sh::NT; ++x) {
+      const bool is_t = (x >= 1 && x <= T) || x > T + 1;
+      const bool is_v = x > T;
+      const void* src = is_v ? (is_t ? p.vt : p.v) : (is_t ? p.kt : p.k);
+      zero_rows(buf + x * Sh::TILE, src == nullptr ? 0 : nk, nkpad);
+    }
+#pragma unroll
+    for (int x = 0; x < Sh::NT; ++x) {
+      const bool is_t = (x >= 1 && x <= T) || x > T + 1;
+      const bool is_v = x > T;
+      const int t = is_v ? x - T - 2 : x - 1;
+      const void* src = is_v ? (is_t ? p.vt : p.v) : (is_t ? p.kt : p.k);
+      if (src == nullptr) continue;
+      const char* wbase = reinterpret_cast<const char*>(static_cast<const float*>(src) + (is_t ? t * p.t_stride : 0) + wofs);
+      char* tile = buf + x * Sh::TILE;
+#pragma unroll
+      for (int j = 0; j < NJ; ++j) {
+        if (j < nj) {
+          if (j * RPI + r0 < nk) { const char* gp = wbase + off[j]; __builtin_amdgcn_global_load_lds(gp, (lds_void_t*)(tile + j * kDmaBytes), 16, 0, 0); }
+        }
+      }
+    }
+  };
+
+  // Rows of masked queries (square mask): exact zeros, lse = -1e4 + log N. The masked
+  // sites of one pass of 64 lanes are fetched in one batch of ds_bpermute.
+  constexpr int NMI = Sh::C4;  // passes for N = 64 (64 rows x C4 float4 / 64 lanes)
+  auto masked_rows = [&](int k, const PcSites& st) {
+    if (km) return;
+    int b, h;
+    seq.bh(k, b, h);
+    const int nmask = N - st.n_phys;
+    int site[NMI];
+#pragma unroll
+    for (int u = 0; u < NMI; ++u) site[u] = __shfl(st.perm, (st.n_phys + (u * 64 + lane) / Sh::C4) & 63, 64);
+#pragma unroll
+    for (int u = 0; u < NMI; ++u) {
+      const int it = u * 64 + lane;
+      if (u * 64 < nmask * Sh::C4 && it < nmask * Sh::C4) {
+        const int64_t off = bnhd(b, site[u], h, N, H, D) + (it % Sh::C4) * 4;
+        if constexpr (!GIVEN_LSE) store4<F32>(p.out, off, 0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+        for (int t = 0; t < T; ++t) store4<F32>(p.tout, t * p.t_stride + off, 0.f, 0.f, 0.f, 0.f);
+        if (!GIVEN_LSE && it % Sh::C4 == 0 && p.lse != nullptr)
+          p.lse[(static_cast<int64_t>(b) * N + site[u]) * H + h] = p.masked_lse;
+      }
+    }
+  };
+
+  auto mask_byte = [&](int k) -> uint32_t {
+    int b, h;
+    seq.bh(k < cnt ? k : 0, b, h);
+    return mreader.byte(b, N, lane);
+  };
+
+  // ---- prologue: item 0 ready, item 1's sites published --------------------------------
+  PcSites cur = pc_sites(mask_byte(0), N);
+  write_slot(0, cur);
+  fill(0, cur);
+  const uint32_t m1 = mask_byte(1);
+  masked_rows(0, cur);
+  __builtin_amdgcn_s_waitcnt(kWaitAll0);
+  PcSites nxt = pc_sites(m1, N);
+  if (cnt > 1) write_slot(1, nxt);
+  __builtin_amdgcn_s_waitcnt(kWaitLgkm0);
+  wg_barrier();
+
+  for (int k = 0; k < cnt; ++k) {
+    // period k: the consumers work on item k; prepare item k+1, publish item k+2's sites.
+    if (k + 1 < cnt) fill(k + 1, nxt);
+    const uint32_t m2 = mask_byte(k + 2);
+    if (k + 1 < cnt) masked_rows(k + 1, nxt);
+    __builtin_amdgcn_s_waitcnt(kWaitAll0);
+    const PcSites nn = pc_sites(m2, N);
+    if (k + 2 < cnt) write_slot(k + 2, nn);
+    __builtin_amdgcn_s_waitcnt(kWaitLgkm0);
+    wg_barrier();
+    nxt = nn;
+  }
+}
+
+// ------------------------------------------------------------------------------------
+// Consumers (waves 0-2)
+// ------------------------------------------------------------------------------------
+
+// One consumer's per-item state: where its query rows are, and their fragments (loaded
+// one item ahead).
+template <int D, int T>
+struct QSet {
+  using Sh = PcShape<D, T>;
+  float qf[Sh::DG];
+  float qtf[Sh::TT][Sh::DG];
+  float lse_in;
+  float oin[Sh::DT][4];
+  int b, h, n_phys, qsite;  // qsite: site of this lane's query (any in-range site if invalid)
+};
+
+template <int DG>
+__device__ __forceinline__ void load_frag_f32(const float* base, int64_t off, float* dst) {
+  if constexpr (DG >= 4) {
+#pragma unroll
+    for (int s = 0; s < DG; s += 4) {
+      const float4 x = *reinterpret_cast<const float4*>(base + off + s);
+      dst[s] = x.x;
+      dst[s + 1] = x.y;
+      dst[s + 2] = x.z;
+      dst[s + 3] = x.w;
+    }
+  } else {
+    const float2 x = *reinterpret_cast<const float2*>(base + off);
+    dst[0] = x.x;
+    dst[1] = x.y;
+  }
+}
+
+template <int D, int T, bool GIVEN_LSE>
+__device__ __forceinline__ void pc_load_q(const FwdParams& p, QSet<D, T>& qs, int b, int h, int n_phys,
+                                          const int16_t* slot_perm, int tile) {
+  using Sh = PcShape<D, T>;
+  const int lane = threadIdx.x & 63;
+  const int g = lane >> 4, c = lane & 15;
+  const int N = p.N, H = p.H;
+  const bool km = p.key_mask != 0;
+  const int jq = tile * 16 + c;
+  const int nq = pc_nq(n_phys, km, N);
+  const int s_raw = km ? jq : static_cast<int>(slot_perm[jq & 63]);
+  const int site = (jq < nq) ? s_raw : 0;  // always an in-range row
+  qs.b = b;
+  qs.h = h;
+  qs.n_phys = n_phys;
+  qs.qsite = site;
+  const int64_t qoff = bnhd(b, site, h, N, H, D) + g * Sh::DG;
+  const float* qt = static_cast<const float*>(p.qt != nullptr ? p.qt : p.q);
+  const int64_t qts = p.qt != nullptr ? p.t_stride : 0;
+  load_frag_f32<Sh::DG>(static_cast<const float*>(p.q), qoff, qs.qf);
+#pragma unroll
+  for (int t = 0; t < T; ++t) load_frag_f32<Sh::DG>(qt, t * qts + qoff, qs.qtf[t]);
+  if constexpr (GIVEN_LSE) {
+    qs.lse_in = p.lse_in[(static_cast<int64_t>(b) * N + site) * H + h];
+    const int64_t obase = bnhd(b, site, h, N, H, D);
+#pragma unroll
+    for (int dt = 0; dt < Sh::DT; ++dt) {
+      const int d0 = (D % 16 == 0) ? dt * 16 + 4 * g : min(dt * 16 + 4 * g, D - 4);
+      const float4 x = *reinterpret_cast<const float4*>(static_cast<const float*>(p.out_in) + obase + d0);
+      qs.oin[dt][0] = x.x;
+      qs.oin[dt][1] = x.y;
+      qs.oin[dt][2] = x.z;
+      qs.oin[dt][3] = x.w;
+    }
+  }
+}
+
+// Compute one 16-query tile of the item described by qs from the key tiles in buf.
+template <int D, int T, bool GIVEN_LSE, bool HAS_E>
+__device__ __forceinline__ void pc_tile(const FwdParams& p, const char* buf, const int16_t* slot_perm,
+                                        const QSet<D, T>& qs, int tile) {
+  using Sh = PcShape<D, T>;
+  constexpr int DG = Sh::DG, DT = Sh::DT, TT = Sh::TT;
+  constexpr int NJT = 4;
+  const int lane = threadIdx.x & 63;
+  const int g = lane >> 4, c = lane & 15;
+  const int N = p.N, H = p.H;
+  const bool km = p.key_mask != 0;
+  const int b = qs.b, h = qs.h;
+  const int nk = pc_nk(qs.n_phys, km, N);
+  const int nq = pc_nq(qs.n_phys, km, N);
+  const bool key_all = km && qs.n_phys == 0;
+  const int njt = (nk + 15) >> 4;
+  const int jq = tile * 16 + c;
+  const bool qvalid = jq < nq;
+  const int qsite = qs.qsite;
+  const float qscale = qvalid ? p.scale : 0.f;
+  const float qtscale = p.qt != nullptr ? qscale : 0.f;
+  float qf[DG], qtf[TT][DG];
+#pragma unroll
+  for (int s = 0; s < DG; ++s) {
+    qf[s] = qs.qf[s] * qscale;
+#pragma unroll
+    for (int t = 0; t < T; ++t) qtf[t][s] = qs.qtf[t][s] * qtscale;
+  }
+
+  const char* Kt0 = buf;                         // K
+  const char* Vt0 = buf + (T + 1) * Sh::TILE;    // V
+
+  // ---- S^T and dS^T: key tile jt+1 is read from LDS while tile jt is multiplied -----
+  // (reads are unconditional, rows < 64 always exist, so the LDS waits are exact counts)
+  v4f sc[NJT];
+  v4f ds[TT][NJT];
+#pragma unroll
+  for (int jt = 0; jt < NJT; ++jt) {
+    sc[jt] = zero4();
+#pragma unroll
+    for (int t = 0; t < T; ++t) ds[t][jt] = zero4();
+  }
+  const int krow = srow_key(c);
+  float kb[2][DG];
+  float ktb[2][TT][DG];
+  auto read_k = [&](int jt, float* kv, float (*ktv)[DG]) {
+    const int r = jt * 16 + krow;
+    if constexpr (DG >= 4) {
+#pragma unroll
+      for (int u = 0; u < DG / 4; ++u) {
+        const int off = swz_off<D>(r, g * (DG / 4) + u);
+        const float4 x = *reinterpret_cast<const float4*>(Kt0 + off);
+        kv[4 * u] = x.x;
+        kv[4 * u + 1] = x.y;
+        kv[4 * u + 2] = x.z;
+        kv[4 * u + 3] = x.w;
+#pragma unroll
+        for (int t = 0; t < T; ++t) {
+          const float4 y = *reinterpret_cast<const float4*>(Kt0 + (1 + t) * Sh::TILE + off);
+          ktv[t][4 * u] = y.x;
+          ktv[t][4 * u + 1] = y.y;
+          ktv[t][4 * u + 2] = y.z;
+          ktv[t][4 * u + 3] = y.w;
+        }
+      }
+    } else {  // D = 8: two floats per lane, half a chunk
+      const int off = swz_off<D>(r, g >> 1) + (g & 1) * 8;
+      const float2 x = *reinterpret_cast<const float2*>(Kt0 + off);
+      kv[0] = x.x;
+      kv[1] = x.y;
+#pragma unroll
+      for (int t = 0; t < T; ++t) {
+        const float2 y = *reinterpret_cast<const float2*>(Kt0 + (1 + t) * Sh::TILE + off);
+        ktv[t][0] = y.x;
+        ktv[t][1] = y.y;
+      }
+    }
+  };
+  read_k(0, kb[0], ktb[0]);
+#pragma unroll
+  for (int jt = 0; jt < NJT; ++jt) {
+    if (jt + 1 < NJT) read_k(jt + 1, kb[(jt + 1) & 1], ktb[(jt + 1) & 1]);
+    if (jt < njt) {
+      const float* kv = kb[jt & 1];
+#pragma unroll
+      for (int s = 0; s < DG; ++s) {
+        sc[jt] = mfma16x4(kv[s], qf[s], sc[jt]);
+#pragma unroll
+        for (int t = 0; t < T; ++t) {
+          ds[t][jt] = mfma16x4(ktb[jt & 1][t][s], qf[s], ds[t][jt]);
+          ds[t][jt] = mfma16x4(kv[s], qtf[t][s], ds[t][jt]);
+        }
+      }
+    }
+  }
+
+  // ---- bias, validity, base-2 scores ---------------------------------------------
+  __amdgpu_buffer_rsrc_t e_rs, et_rs[TT];
+  int e_row = 0;
+  if constexpr (HAS_E) {
+    const int64_t wstride = static_cast<int64_t>(N) * N * H;
+    const int64_t ebytes = wstride * 4;
+    e_rs = make_rsrc(p.e != nullptr ? static_cast<const float*>(p.e) + b * wstride : nullptr,
+                     p.e != nullptr ? ebytes : 0);
+#pragma unroll
+    for (int t = 0; t < T; ++t)
+      et_rs[t] = make_rsrc(p.et != nullptr ? static_cast<const float*>(p.et) + t * p.et_stride + b * wstride : nullptr,
+                           p.et != nullptr ? ebytes : 0);
+    e_row = static_cast<int>(qsite * p.e_sq + h * p.e_sh);
+  }
+  const int e_oob = static_cast<int>(static_cast<int64_t>(N) * N * H * 4);
+  float mx = -INFINITY;
+#pragma unroll
+  for (int jt = 0; jt < NJT; ++jt) {
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int j = jt * 16 + 4 * r + g;
+      const bool valid = jt < njt && j < nk;
+      float sv = sc[jt][r];
+      if constexpr (HAS_E) {
+        if (jt < njt) {
+          const int ks = key_all ? j : static_cast<int>(slot_perm[j & 63]);
+          const int eo = (valid && qvalid) ? (e_row + ks * static_cast<int>(p.e_sk)) * 4 : e_oob;
+          sv += buf_load1(e_rs, eo);
+#pragma unroll
+          for (int t = 0; t < T; ++t) ds[t][jt][r] += buf_load1(et_rs[t], eo);
+        }
+      }
+      sc[jt][r] = valid ? sv * kLog2e : -INFINITY;
+#pragma unroll
+      for (int t = 0; t < T; ++t) ds[t][jt][r] = valid ? ds[t][jt][r] : 0.f;
+      mx = fmaxf(mx, sc[jt][r]);
+    }
+  }
+
+  float lsum = 0.f;
+  if constexpr (GIVEN_LSE) {
+    const float lse2 = qs.lse_in * kLog2e;
+#pragma unroll
+    for (int jt = 0; jt < NJT; ++jt)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) sc[jt][r] = fast_exp2(sc[jt][r] - lse2);
+  } else {
+    mx = group_max(mx);
+#pragma unroll
+    for (int jt = 0; jt < NJT; ++jt)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        sc[jt][r] = fast_exp2(sc[jt][r] - mx);
+        lsum += sc[jt][r];
+      }
+  }
+  float mu[TT];
+#pragma unroll
+  for (int t = 0; t < T; ++t) {
+    mu[t] = 0.f;
+#pragma unroll
+    for (int jt = 0; jt < NJT; ++jt) {
+      ds[t][jt] *= sc[jt];
+      mu[t] += (ds[t][jt][0] + ds[t][jt][1]) + (ds[t][jt][2] + ds[t][jt][3]);
+    }
+  }
+
+  // ---- O^T, A^T, C^T: step r of tile jt contracts keys jt*16 + 4r + (0..3) --------
+  v4f o[DT];
+  v4f at[TT][DT];
+  v4f ct[TT][DT];
+#pragma unroll
+  for (int dt = 0; dt < DT; ++dt) {
+    o[dt] = zero4();
+#pragma unroll
+    for (int t = 0; t < T; ++t) at[t][dt] = ct[t][dt] = zero4();
+  }
+  const bool colok = D % 16 == 0 || c < D;
+  float vb[2][4][DT];
+  float vtb[2][TT][4][DT];
+  auto read_v = [&](int jt, float (*va)[DT], float (*vta)[4][DT]) {
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int row = jt * 16 + 4 * r + g;
+#pragma unroll
+      for (int dt = 0; dt < DT; ++dt) {
+        const int col = (D % 16 == 0) ? dt * 16 + c : min(c, D - 1);
+        const int off = swz_off<D>(row, col >> 2) + (col & 3) * 4;
+        const float x = *reinterpret_cast<const float*>(Vt0 + off);
+        va[r][dt] = colok ? x : 0.f;
+#pragma unroll
+        for (int t = 0; t < T; ++t) {
+          const float y = *reinterpret_cast<const float*>(Vt0 + (1 + t) * Sh::TILE + off);
+          vta[t][r][dt] = colok ? y : 0.f;
+        }
+      }
+    }
+  };
+  read_v(0, vb[0], vtb[0]);
+#pragma unroll
+  for (int jt = 0; jt < NJT; ++jt) {
+    if (jt + 1 < NJT) read_v(jt + 1, vb[(jt + 1) & 1], vtb[(jt + 1) & 1]);
+    if (jt < njt) {
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        if (jt * 16 + 4 * r < nk) {
+#pragma unroll
+          for (int dt = 0; dt < DT; ++dt) {
+            const float va = vb[jt & 1][r][dt];
+            if constexpr (!GIVEN_LSE) o[dt] = mfma16x4(va, sc[jt][r], o[dt]);
+#pragma unroll
+            for (int t = 0; t < T; ++t) {
+              at[t][dt] = mfma16x4(va, ds[t][jt][r], at[t][dt]);
+              ct[t][dt] = mfma16x4(vtb[jt & 1][t][r][dt], sc[jt][r], ct[t][dt]);
+            }
+          }
+        }
+      }
+    }
+  }
+
+  float inv = 1.f, ltot = 0.f;
+  if constexpr (!GIVEN_LSE) {
+    ltot = group_sum(lsum);
+    inv = 1.f / ltot;
+  }
+  float mut[TT];
+#pragma unroll
+  for (int t = 0; t < T; ++t) mut[t] = group_sum(mu[t]) * inv;
+
+  // ---- stores: unconditional, invalid lanes past the walker's last record ------------
+  const int64_t wrow = static_cast<int64_t>(N) * H * D;  // floats per walker
+  const int obytes = static_cast<int>(wrow * 4);
+  const int obase = (qsite * H + h) * D;
+  if constexpr (!GIVEN_LSE) {
+    const __amdgpu_buffer_rsrc_t o_rs = make_rsrc(static_cast<float*>(p.out) + b * wrow, obytes);
+#pragma unroll
+    for (int dt = 0; dt < DT; ++dt) {
+      const int d0 = dt * 16 + 4 * g;
+      const int voff = (qvalid && (D % 16 == 0 || d0 < D)) ? (obase + d0) * 4 : obytes;
+      buf_store4(o_rs, voff, o[dt][0] * inv, o[dt][1] * inv, o[dt][2] * inv, o[dt][3] * inv);
+    }
+    const int lbytes = N * H * 4;
+    const __amdgpu_buffer_rsrc_t l_rs =
+        make_rsrc(p.lse != nullptr ? p.lse + static_cast<int64_t>(b) * N * H : nullptr, p.lse != nullptr ? lbytes : 0);
+    const int lvoff = (qvalid && g == 0) ? (qsite * H + h) * 4 : lbytes;
+    __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint((mx + log2f(ltot)) * kLn2), l_rs, lvoff, 0, 0);
+  }
+#pragma unroll
+  for (int t = 0; t < T; ++t) {
+    const __amdgpu_buffer_rsrc_t t_rs = make_rsrc(static_cast<float*>(p.tout) + t * p.t_stride + b * wrow, obytes);
+#pragma unroll
+    for (int dt = 0; dt < DT; ++dt) {
+      const int d0 = dt * 16 + 4 * g;
+      const int voff = (qvalid && (D % 16 == 0 || d0 < D)) ? (obase + d0) * 4 : obytes;
+      float tv[4];
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const float orr = GIVEN_LSE ? qs.oin[dt][r] : o[dt][r] * inv;
+        tv[r] = (at[t][dt][r] + ct[t][dt][r]) * inv - mut[t] * orr;
+      }
+      buf_store4(t_rs, voff, tv[0], tv[1], tv[2], tv[3]);
+    }
+  }
+}
+
+template <int D, int T, bool GIVEN_LSE, bool HAS_E>
+__device__ __forceinline__ void pc_consumer(const FwdParams& p, const char* lds, const ItemSeq& seq, int cnt) {
+  using Sh = PcShape<D, T>;
+  const int wave = threadIdx.x >> 6;
+  const int N = p.N;
+  const bool km = p.key_mask != 0;
+  const char* const slots = lds + 2 * Sh::BUF;
+  auto slot_perm = [&](int k) { return reinterpret_cast<const int16_t*>(slots + (k % kSlots) * kSlotBytes); };
+  auto slot_n = [&](int k) { return reinterpret_cast<const int*>(slots + (k % kSlots) * kSlotBytes + 128)[0]; };
+
+  // Prefetch item k's query fragments (item k-1's when k is past the end, which keeps
+  // the number of loads per period fixed).
+  auto prefetch = [&](QSet<D, T>& qs, const QSet<D, T>& prev, int k) {
+    if (k < cnt) {
+      int b, h;
+      seq.bh(k, b, h);
+      pc_load_q<D, T, GIVEN_LSE>(p, qs, b, h, slot_n(k), slot_perm(k), wave);
+    } else {
+      pc_load_q<D, T, GIVEN_LSE>(p, qs, prev.b, prev.h, 0, slot_perm(k - 1), wave);
+      qs.n_phys = prev.n_phys;
+    }
+  };
+
+  auto compute = [&](const QSet<D, T>& qs, int k) {
+    const char* buf = lds + (k & 1) * Sh::BUF;
+    const int nq = pc_nq(qs.n_phys, km, N);
+    if (wave * 16 < nq) pc_tile<D, T, GIVEN_LSE, HAS_E>(p, buf, slot_perm(k), qs, wave);
+    // A fourth query tile (n > 48) goes to consumer 0, with its fragments loaded here.
+    if (wave == 0 && 3 * 16 < nq) {
+      QSet<D, T> q3;
+      pc_load_q<D, T, GIVEN_LSE>(p, q3, qs.b, qs.h, qs.n_phys, slot_perm(k), 3);
+      pc_tile<D, T, GIVEN_LSE, HAS_E>(p, buf, slot_perm(k), q3, 3);
+    }
+    __builtin_amdgcn_s_waitcnt(kWaitLgkm0);
+  };
+
+  QSet<D, T> qa, qb;
+  wg_barrier();  // item 0 ready, item 1's sites published
+  {
+    int b, h;
+    seq.bh(0, b, h);
+    pc_load_q<D, T, GIVEN_LSE>(p, qa, b, h, slot_n(0), slot_perm(0), wave);
+  }
+  for (int k = 0; k < cnt; k += 2) {
+    prefetch(qb, qa, k + 1);
+    compute(qa, k);
+    wg_barrier();
+    if (k + 1 >= cnt) break;
+    prefetch(qa, qb, k + 2);
+    compute(qb, k + 1);
+    wg_barrier();
+  }
+}
+
+template <int D, int T, bool GIVEN_LSE, bool HAS_E>
+__global__ void __launch_bounds__(256, 2) mhsea_fwd_pc_kernel(const FwdParams p) {
+  using Sh = PcShape<D, T>;
+  extern __shared__ float4 smem4[];
+  char* const lds = reinterpret_cast<char*>(smem4);
+  const uint32_t nitems = static_cast<uint32_t>(p.B) * static_cast<uint32_t>(p.H);
+  const uint32_t G = gridDim.x;
+  const uint32_t L = static_cast<uint32_t>(xcd_logical_block(blockIdx.x, G));
+  if (L >= nitems) return;  // workgroup-uniform
+  const ItemSeq seq{L, G, nitems, static_cast<uint32_t>(p.H)};
+  const int cnt = static_cast<int>((nitems - L + G - 1) / G);
+  if ((threadIdx.x >> 6) == kProducerWave)
+    pc_producer<D, T, GIVEN_LSE>(p, lds, seq, cnt);
+  else
+    pc_consumer<D, T, GIVEN_LSE, HAS_E>(p, lds, seq, cnt);
+  (void)Sh::LDS;
+}
+
+template <int D, int T, bool GIVEN_LSE, bool HAS_E>
+hipError_t launch_pc_t(const FwdParams& p, hipStream_t stream) {
+  using Sh = PcShape<D, T>;
+  auto kern = mhsea_fwd_pc_kernel<D, T, GIVEN_LSE, HAS_E>;
+  const size_t lds = Sh::LDS;
+  if (lds > 64 * 1024) {
+    hipError_t err = hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
+                                         hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(lds));
+    if (err != hipSuccess) return err;
+  }
+  static int per_cu = 0;
+  if (per_cu == 0) {
+    int n = 0;
+    hipError_t err = hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, reinterpret_cast<const void*>(kern), 256, lds);
+    if (err != hipSuccess) return err;
+    per_cu = n > 0 ? n : 1;
+  }
+  int cus = 0;
+  hipError_t err = device_cu_count(&cus);
+  if (err != hipSuccess) return err;
+  const int64_t nitems = static_cast<int64_t>(p.B) * p.H;
+  int64_t grid = static_cast<int64_t>(cus) * per_cu;
+  if (grid > nitems) grid = nitems;
+  hipLaunchKernelGGL(kern, dim3(static_cast<unsigned>(grid)), dim3(256), lds, stream, p);
+  return hipGetLastError();
+}
+
+// Shapes served: two workgroups per CU must fit their double-buffered key tiles in LDS.
+template <int D, int T>
+constexpr bool pc_shape_ok() {
+  return PcShape<D, T>::LDS <= 80 * 1024;
+}
+
+template <int D, int T, bool GIVEN_LSE>
+hipError_t dispatch_e(const FwdParams& p, hipStream_t stream) {
+  if constexpr (pc_shape_ok<D, T>()) {
+    if (p.e != nullptr || p.et != nullptr) return launch_pc_t<D, T, GIVEN_LSE, true>(p, stream);
+    return launch_pc_t<D, T, GIVEN_LSE, false>(p, stream);
+  }
+  return hipErrorInvalidValue;
+}
+
+template <int D>
+hipError_t dispatch_t(const FwdParams& p, int T, bool given_lse, hipStream_t stream) {
+  if (given_lse) {
+    if (T == 1) return dispatch_e<D, 1, true>(p, stream);
+    if (T == 2) return dispatch_e<D, 2, true>(p, stream);
+    return hipErrorInvalidValue;
+  }
+  if (T == 0) return dispatch_e<D, 0, false>(p, stream);
+  if (T == 1) return dispatch_e<D, 1, false>(p, stream);
+  if (T == 2) return dispatch_e<D, 2, false>(p, stream);
+  return hipErrorInvalidValue;
+}
+
+}  // namespace
+
+bool pc_fwd_supported(int N, int H, int D, int T, int dtype) {
+  if (dtype != 0 || N > 64 || T > 2) return false;
+  // Per-walker buffer resources: the walker's bias and output slices must stay below 2 GiB.
+  if (static_cast<int64_t>(N) * N * H * 4 >= (int64_t(1) << 31)) return false;
+  if (static_cast<int64_t>(N) * H * D * 4 >= (int64_t(1) << 31)) return false;
+  switch (D) {
+    case 8: return pc_shape_ok<8, 0>() && (T < 1 || pc_shape_ok<8, 1>()) && (T < 2 || pc_shape_ok<8, 2>());
+    case 16: return (T < 1 || pc_shape_ok<16, 1>()) && (T < 2 || pc_shape_ok<16, 2>());
+    case 32: return (T < 1 || pc_shape_ok<32, 1>()) && (T < 2 || pc_shape_ok<32, 2>());
+    default: return false;  // D = 64: the key operands of a tile no longer fit the registers
+  }
+}
+
+hipError_t launch_fwd_pc(const FwdParams& p, int D, int T, bool given_lse, hipStream_t stream) {
+  switch (D) {
+    case 8: return dispatch_t<8>(p, T, given_lse, stream);
+    case 16: return dispatch_t<16>(p, T, given_lse, stream);
+    case 32: return dispatch_t<32>(p, T, given_lse, stream);
+    default: return hipErrorInvalidValue;
+  }
+}
+
+}  // namespace hz

@@ -61,10 +61,13 @@ __device__ __forceinline__ void put4(float* dst, float4 x, bool keep) {
       make_float4(keep ? x.x : 0.f, keep ? x.y : 0.f, keep ? x.z : 0.f, keep ? x.w : 0.f);
 }
 
-// Walker / head of item `it` (items are ordered walker-major).
-__device__ __forceinline__ void item_bh(int64_t it, int H, int& b, int& h) {
-  b = static_cast<int>(it / H);
-  h = static_cast<int>(it % H);
+// Walker / head of item `it` (items are ordered walker-major). Item indices are 32-bit
+// (the host checks B*H < 2^31): 64-bit division costs registers that would otherwise spill,
+// and a scratch reload inside the loop waits (in-order vmcnt) on the prefetch loads.
+__device__ __forceinline__ void item_bh(uint32_t it, uint32_t H, int& b, int& h) {
+  const uint32_t bq = it / H;
+  b = static_cast<int>(bq);
+  h = static_cast<int>(it - bq * H);
 }
 
 // Compacted-site bookkeeping of one item, lane-resident: the permutation (lane j holds
@@ -112,9 +115,9 @@ __global__ void __launch_bounds__(256, (StreamShape<D, T>::kWavesPerEu))
   float* const Vts = Kts + T * Sh::kTileFloats;
 
   const int N = p.N, H = p.H;
-  const int64_t nitems = static_cast<int64_t>(p.B) * H;
-  const int64_t stride = gridDim.x;
-  int64_t item = blockIdx.x;
+  const uint32_t nitems = static_cast<uint32_t>(p.B) * static_cast<uint32_t>(H);
+  const uint32_t stride = gridDim.x;
+  uint32_t item = blockIdx.x;
   if (item >= nitems) return;  // workgroup-uniform
 
   const int tid = threadIdx.x;
@@ -165,16 +168,18 @@ __global__ void __launch_bounds__(256, (StreamShape<D, T>::kWavesPerEu))
     if constexpr (GIVEN_LSE) lse2n = p.lse_in[(static_cast<int64_t>(b) * N + qload) * H + h];
   };
 
-  auto load_mask_byte = [&](int b) -> uint32_t {
-    return lane < N ? static_cast<uint32_t>(p.mask[static_cast<int64_t>(b) * N + lane]) : 0u;
-  };
+  // Mask bytes through a buffer resource: walker offset in an SGPR, lane offset in a VGPR,
+  // lanes >= N read 0 (out-of-range records). Nothing 64-bit stays live in VGPRs across
+  // the loop.
+  const MaskReader mreader(p.mask, static_cast<int64_t>(p.B) * N);
+  auto load_mask_byte = [&](int b) -> uint32_t { return mreader.byte(b, N, lane); };
 
   // ---- prologue: item 0 loads in flight, item 1 mask in flight -------------------------
   int b, h;
   item_bh(item, H, b, h);
   Sites cur = make_sites(load_mask_byte(b), N);
   issue_item_loads(b, h, cur);
-  int64_t nxt = item + stride;
+  uint32_t nxt = item + stride;
   uint32_t mnext = 0;
   if (nxt < nitems) {
     int bn, hn;
@@ -226,7 +231,7 @@ __global__ void __launch_bounds__(256, (StreamShape<D, T>::kWavesPerEu))
       item_bh(nxt, H, b, h);
       cur = make_sites(mnext, N);
       issue_item_loads(b, h, cur);
-      const int64_t nn = nxt + stride;
+      const uint32_t nn = nxt + stride;
       if (nn < nitems) {
         int bn, hn;
         item_bh(nn, H, bn, hn);
