@@ -8,10 +8,11 @@
 //     compacted query list and runs S^T = K Q^T, the exact softmax (all keys in one tile)
 //     and O^T += V^T P^T on the fp32 matrix cores (v_mfma_f32_16x16x4_f32), with the
 //     tangent products dS^T = Kt Q^T + K Qt^T, A^T = V^T (P o dS)^T, C^T = Vt^T P^T;
-//   - the producer gathers item k+1's physical key rows (K, Kt, V, Vt) from HBM straight
-//     into LDS buffer (k+1)%2 with global_load_lds_dwordx4 (no registers hold them),
-//     zero-fills the rows of the last partial 16-key tile, writes item k+1's masked output
-//     rows (exact zeros, lse = -1e4 + log N) and reads item k+2's mask row.
+//   - the producer gathers item k+1's physical key rows (K, Kt, V, Vt) from HBM into
+//     LDS buffer (k+1)%2 (all 16-byte reads of the item in flight at once, one wait, then
+//     swizzled LDS writes), zero-fills the rows of the last partial 16-key tile, writes
+//     item k+1's masked output rows (exact zeros, lse = -1e4 + log N) and reads item
+//     k+2's mask row.
 // A single s_barrier ends a period. The producer publishes each item's compacted site
 // list in one of four LDS slots two periods ahead, so the consumers can prefetch their
 // query fragments one item ahead into registers. Consumers alternate two register sets
@@ -34,13 +35,12 @@
 namespace hz {
 namespace {
 
-typedef __attribute__((address_space(3))) void lds_void_t;
 typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
 
 constexpr int kProducerWave = 3;
 constexpr int kSlots = 4;
 constexpr int kSlotBytes = 144;  // int16 perm[64], int32 n_phys at byte 128
-constexpr int kDmaBytes = 1024;  // one global_load_lds_dwordx4 wave instruction
+constexpr int kDmaBytes = 1024;  // bytes one 16-byte-per-lane wave instruction moves
 
 template <int D, int T>
 struct PcShape {
@@ -168,24 +168,25 @@ __device__ __forceinline__ void pc_producer(const FwdParams& p, char* lds, const
     }
   };
 
-  // Item k's key tiles. The DMA lane mapping is the same for every tensor: instruction j
-  // writes tile bytes [1024 j, 1024 j + 1024), lane l the 16 bytes at 1024 j + 16 l, i.e.
-  // chunk position pch of row r_j; it reads the row's swizzled source chunk. The per-lane
-  // byte offsets inside the walker's slice are computed once per item (one batch of
-  // ds_bpermute), and each tensor then costs one global_load_lds per 1 KiB from a scalar
-  // base address. The padding rows of the last partial 16-key tile are zeroed first (no
-  // LDS-DMA is in flight to them).
-  constexpr int RPI = kDmaBytes / Sh::ROWB;  // rows per DMA instruction
-  constexpr int NJ = 64 / RPI;               // DMA instructions per full 64-row tile
-  auto fill = [&](int k, const PcSites& st) {
+  // Item k's key tiles travel in two steps one period apart: load() issues every 16-byte
+  // global read of the item's physical key rows into registers (one wave instruction per
+  // 1 KiB of a tile), and a period later, after one wait, store() writes them to LDS. So
+  // the load latency of an item overlaps a whole period of the consumers' work.
+  // Instruction j of a tile covers tile bytes [1024 j, 1024 j + 1024); lane l holds the
+  // 16 bytes at 1024 j + 16 l, i.e. chunk position pch of row r_j, which comes from the
+  // row's swizzled source chunk. The per-lane byte offsets inside the walker's slice are
+  // computed once per item (one batch of ds_bpermute); each tensor then reads from a
+  // scalar base address. A null tangent stages zeros.
+  constexpr int RPI = kDmaBytes / Sh::ROWB;  // rows per instruction
+  constexpr int NJ = 64 / RPI;               // instructions per full 64-row tile
+  float4 stage[Sh::NT][NJ];
+  const int r0 = lane * 16 / Sh::ROWB;
+  auto load = [&](int k, const PcSites& st) {
     int b, h;
     seq.bh(k, b, h);
-    char* buf = lds + (k & 1) * Sh::BUF;
     const int nk = pc_nk(st.n_phys, km, N);
-    const int nkpad = (nk + 15) & ~15;
     const int kperm = (km && st.n_phys == 0) ? lane : st.perm;
     const int pch = (lane * 16 % Sh::ROWB) >> 4;
-    const int r0 = lane * 16 / Sh::ROWB;
     uint32_t off[NJ];
 #pragma unroll
     for (int j = 0; j < NJ; ++j) {
@@ -194,29 +195,36 @@ __device__ __forceinline__ void pc_producer(const FwdParams& p, char* lds, const
       const int c = pch ^ swz<D>(r);
       off[j] = static_cast<uint32_t>(((site * H + h) * D) * 4 + c * 16);
     }
-    const int nj = (nk * Sh::ROWB + kDmaBytes - 1) / kDmaBytes;
     const int64_t wofs = static_cast<int64_t>(b) * N * H * D;  // walker offset, elements
 #pragma unroll
     for (int x = 0; x < Sh::NT; ++x) {
       const bool is_t = (x >= 1 && x <= T) || x > T + 1;
       const bool is_v = x > T;
-      const void* src = is_v ? (is_t ? p.vt : p.v) : (is_t ? p.kt : p.k);
-      zero_rows(buf + x * Sh::TILE, src == nullptr ? 0 : nk, nkpad);
-    }
-#pragma unroll
-    for (int x = 0; x < Sh::NT; ++x) {
-      const bool is_t = (x >= 1 && x <= T) || x > T + 1;
-      const bool is_v = x > T;
       const int t = is_v ? x - T - 2 : x - 1;
-      const void* src = is_v ? (is_t ? p.vt : p.v) : (is_t ? p.kt : p.k);
-      if (src == nullptr) continue;
-      const char* wbase = reinterpret_cast<const char*>(static_cast<const float*>(src) + (is_t ? t * p.t_stride : 0) + wofs);
-      char* tile = buf + x * Sh::TILE;
+      const void* src0 = is_v ? (is_t ? p.vt : p.v) : (is_t ? p.kt : p.k);
+      const void* src = src0 != nullptr ? src0 : p.k;
+      const char* wbase = reinterpret_cast<const char*>(static_cast<const float*>(src) +
+                                                        (is_t && src0 != nullptr ? t * p.t_stride : 0) + wofs);
 #pragma unroll
       for (int j = 0; j < NJ; ++j) {
-        if (j < nj) {
-          if (j * RPI + r0 < nk) { const char* gp = wbase + off[j]; __builtin_amdgcn_global_load_lds(gp, (lds_void_t*)(tile + j * kDmaBytes), 16, 0, 0); }
-        }
+        float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
+        if (j * RPI < nk && j * RPI + r0 < nk) v = *reinterpret_cast<const float4*>(wbase + off[j]);
+        stage[x][j] = src0 != nullptr ? v : make_float4(0.f, 0.f, 0.f, 0.f);
+      }
+    }
+  };
+  auto store = [&](int k, const PcSites& st) {
+    const int nk = pc_nk(st.n_phys, km, N);
+    const int nkpad = (nk + 15) & ~15;
+    char* buf = lds + (k & 1) * Sh::BUF;
+#pragma unroll
+    for (int x = 0; x < Sh::NT; ++x) {
+      char* tile = buf + x * Sh::TILE;
+      zero_rows(tile, nk, nkpad);
+#pragma unroll
+      for (int j = 0; j < NJ; ++j) {
+        if (j * RPI < nk && j * RPI + r0 < nk)
+          *reinterpret_cast<float4*>(tile + j * kDmaBytes + lane * 16) = stage[x][j];
       }
     }
   };
@@ -252,30 +260,40 @@ __device__ __forceinline__ void pc_producer(const FwdParams& p, char* lds, const
     return mreader.byte(b, N, lane);
   };
 
-  // ---- prologue: item 0 ready, item 1's sites published --------------------------------
+  // ---- prologue: item 0 in LDS, item 1's sites published and its rows in flight --------
   PcSites cur = pc_sites(mask_byte(0), N);
   write_slot(0, cur);
-  fill(0, cur);
-  const uint32_t m1 = mask_byte(1);
+  load(0, cur);
+  uint32_t m = mask_byte(1);
   masked_rows(0, cur);
   __builtin_amdgcn_s_waitcnt(kWaitAll0);
-  PcSites nxt = pc_sites(m1, N);
-  if (cnt > 1) write_slot(1, nxt);
+  store(0, cur);
+  cur = pc_sites(m, N);  // item 1
+  if (cnt > 1) {
+    write_slot(1, cur);
+    load(1, cur);
+    masked_rows(1, cur);
+  }
+  m = mask_byte(2);
   __builtin_amdgcn_s_waitcnt(kWaitLgkm0);
   wg_barrier();
 
   for (int k = 0; k < cnt; ++k) {
-    // period k: the consumers work on item k; prepare item k+1, publish item k+2's sites.
-    if (k + 1 < cnt) fill(k + 1, nxt);
-    const uint32_t m2 = mask_byte(k + 2);
-    if (k + 1 < cnt) masked_rows(k + 1, nxt);
+    // period k: the consumers work on item k. Item k+1's rows (in flight since period
+    // k-1) go to LDS, item k+2's sites are published and its rows start loading.
     __builtin_amdgcn_s_waitcnt(kWaitAll0);
-    const PcSites nn = pc_sites(m2, N);
-    if (k + 2 < cnt) write_slot(k + 2, nn);
+    if (k + 1 < cnt) store(k + 1, cur);
+    cur = pc_sites(m, N);  // item k+2
+    if (k + 2 < cnt) {
+      write_slot(k + 2, cur);
+      load(k + 2, cur);
+      masked_rows(k + 2, cur);
+    }
+    m = mask_byte(k + 3);
     __builtin_amdgcn_s_waitcnt(kWaitLgkm0);
     wg_barrier();
-    nxt = nn;
   }
+  __builtin_amdgcn_s_waitcnt(kWaitAll0);
 }
 
 // ------------------------------------------------------------------------------------
@@ -349,13 +367,39 @@ __device__ __forceinline__ void pc_load_q(const FwdParams& p, QSet<D, T>& qs, in
   }
 }
 
-// Compute one 16-query tile of the item described by qs from the key tiles in buf.
-template <int D, int T, bool GIVEN_LSE, bool HAS_E>
+// Forces the compiler to materialise v here (and so to wait for its load, if any),
+// without emitting an instruction.
+__device__ __forceinline__ void settle(float& v) { asm volatile("" : "+v"(v)); }
+
+template <int D, int T, bool GIVEN_LSE>
+__device__ __forceinline__ void settle_q(QSet<D, T>& qs) {
+  using Sh = PcShape<D, T>;
+#pragma unroll
+  for (int s = 0; s < Sh::DG; ++s) {
+    settle(qs.qf[s]);
+#pragma unroll
+    for (int t = 0; t < T; ++t) settle(qs.qtf[t][s]);
+  }
+  if constexpr (GIVEN_LSE) {
+    settle(qs.lse_in);
+#pragma unroll
+    for (int dt = 0; dt < Sh::DT; ++dt)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) settle(qs.oin[dt][r]);
+  }
+}
+
+// Compute one 16-query tile of the item described by qs from the key tiles in buf, with
+// NJ = ceil(n_keys / 16) key tiles (a compile-time count, so every loop is unrolled
+// without branches and the scheduler can interleave the tiles' loads and products).
+// pf() issues the next item's query prefetch; it runs after this tile's own global loads
+// (bias) are issued, so waiting for those never waits for the prefetch. sq() settles
+// the prefetch before this tile's stores, so the next period never waits for them.
+template <int D, int T, bool GIVEN_LSE, bool HAS_E, int NJ, class PF, class SQ>
 __device__ __forceinline__ void pc_tile(const FwdParams& p, const char* buf, const int16_t* slot_perm,
-                                        const QSet<D, T>& qs, int tile) {
+                                        const QSet<D, T>& qs, int tile, PF&& pf, SQ&& sq) {
   using Sh = PcShape<D, T>;
   constexpr int DG = Sh::DG, DT = Sh::DT, TT = Sh::TT;
-  constexpr int NJT = 4;
   const int lane = threadIdx.x & 63;
   const int g = lane >> 4, c = lane & 15;
   const int N = p.N, H = p.H;
@@ -364,10 +408,39 @@ __device__ __forceinline__ void pc_tile(const FwdParams& p, const char* buf, con
   const int nk = pc_nk(qs.n_phys, km, N);
   const int nq = pc_nq(qs.n_phys, km, N);
   const bool key_all = km && qs.n_phys == 0;
-  const int njt = (nk + 15) >> 4;
   const int jq = tile * 16 + c;
   const bool qvalid = jq < nq;
   const int qsite = qs.qsite;
+
+  // ---- bias (and its tangents) for this lane's 4 NJ scores: issued first -------------
+  float ev[NJ][4];
+  float etv[TT][NJ][4];
+  if constexpr (HAS_E) {
+    const int64_t wstride = static_cast<int64_t>(N) * N * H;
+    const int64_t ebytes = wstride * 4;
+    const __amdgpu_buffer_rsrc_t e_rs = make_rsrc(
+        p.e != nullptr ? static_cast<const float*>(p.e) + b * wstride : nullptr, p.e != nullptr ? ebytes : 0);
+    const int e_row = static_cast<int>(qsite * p.e_sq + h * p.e_sh);
+    const int e_oob = static_cast<int>(ebytes);
+#pragma unroll
+    for (int jt = 0; jt < NJ; ++jt)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int j = jt * 16 + 4 * r + g;
+        const int ks = key_all ? j : static_cast<int>(slot_perm[j & 63]);
+        const int eo = (j < nk && qvalid) ? (e_row + ks * static_cast<int>(p.e_sk)) * 4 : e_oob;
+        ev[jt][r] = buf_load1(e_rs, eo);
+#pragma unroll
+        for (int t = 0; t < T; ++t) {
+          const __amdgpu_buffer_rsrc_t et_rs =
+              make_rsrc(p.et != nullptr ? static_cast<const float*>(p.et) + t * p.et_stride + b * wstride : nullptr,
+                        p.et != nullptr ? ebytes : 0);
+          etv[t][jt][r] = buf_load1(et_rs, eo);
+        }
+      }
+  }
+  pf();
+
   const float qscale = qvalid ? p.scale : 0.f;
   const float qtscale = p.qt != nullptr ? qscale : 0.f;
   float qf[DG], qtf[TT][DG];
@@ -378,104 +451,113 @@ __device__ __forceinline__ void pc_tile(const FwdParams& p, const char* buf, con
     for (int t = 0; t < T; ++t) qtf[t][s] = qs.qtf[t][s] * qtscale;
   }
 
-  const char* Kt0 = buf;                         // K
-  const char* Vt0 = buf + (T + 1) * Sh::TILE;    // V
+  const char* K0 = buf;                        // K, then Kt[t] at +(1+t) tiles
+  const char* V0 = buf + (T + 1) * Sh::TILE;   // V, then Vt[t] at +(1+t) tiles
 
-  // ---- S^T and dS^T: key tile jt+1 is read from LDS while tile jt is multiplied -----
-  // (reads are unconditional, rows < 64 always exist, so the LDS waits are exact counts)
-  v4f sc[NJT];
-  v4f ds[TT][NJT];
+  // ---- S^T and dS^T -------------------------------------------------------------------
+  // Every key row of this item's tiles is read up front (the compiler fence keeps the
+  // reads here), then the three product chains run tile-interleaved, so consecutive
+  // matrix-core instructions never depend on each other.
+  const int krow = srow_key(c);
+  float kv[NJ][DG];
+  float ktv[NJ][TT][DG];
+  if constexpr (DG >= 4) {
 #pragma unroll
-  for (int jt = 0; jt < NJT; ++jt) {
+    for (int u = 0; u < DG / 4; ++u)
+#pragma unroll
+      for (int jt = 0; jt < NJ; ++jt) {
+        const int off = swz_off<D>(jt * 16 + krow, g * (DG / 4) + u);
+        const float4 x = *reinterpret_cast<const float4*>(K0 + off);
+        kv[jt][4 * u] = x.x;
+        kv[jt][4 * u + 1] = x.y;
+        kv[jt][4 * u + 2] = x.z;
+        kv[jt][4 * u + 3] = x.w;
+      }
+#pragma unroll
+    for (int t = 0; t < T; ++t)
+#pragma unroll
+      for (int u = 0; u < DG / 4; ++u)
+#pragma unroll
+        for (int jt = 0; jt < NJ; ++jt) {
+          const int off = swz_off<D>(jt * 16 + krow, g * (DG / 4) + u);
+          const float4 y = *reinterpret_cast<const float4*>(K0 + (1 + t) * Sh::TILE + off);
+          ktv[jt][t][4 * u] = y.x;
+          ktv[jt][t][4 * u + 1] = y.y;
+          ktv[jt][t][4 * u + 2] = y.z;
+          ktv[jt][t][4 * u + 3] = y.w;
+        }
+  } else {  // D = 8: two floats per lane, half a chunk
+#pragma unroll
+    for (int jt = 0; jt < NJ; ++jt) {
+      const int off = swz_off<D>(jt * 16 + krow, g >> 1) + (g & 1) * 8;
+      const float2 x = *reinterpret_cast<const float2*>(K0 + off);
+      kv[jt][0] = x.x;
+      kv[jt][1] = x.y;
+#pragma unroll
+      for (int t = 0; t < T; ++t) {
+        const float2 y = *reinterpret_cast<const float2*>(K0 + (1 + t) * Sh::TILE + off);
+        ktv[jt][t][0] = y.x;
+        ktv[jt][t][1] = y.y;
+      }
+    }
+  }
+  compiler_fence();
+  v4f sc[NJ];
+  v4f ds[TT][NJ];
+#pragma unroll
+  for (int jt = 0; jt < NJ; ++jt) {
     sc[jt] = zero4();
 #pragma unroll
     for (int t = 0; t < T; ++t) ds[t][jt] = zero4();
   }
-  const int krow = srow_key(c);
-  float kb[2][DG];
-  float ktb[2][TT][DG];
-  auto read_k = [&](int jt, float* kv, float (*ktv)[DG]) {
-    const int r = jt * 16 + krow;
-    if constexpr (DG >= 4) {
 #pragma unroll
-      for (int u = 0; u < DG / 4; ++u) {
-        const int off = swz_off<D>(r, g * (DG / 4) + u);
-        const float4 x = *reinterpret_cast<const float4*>(Kt0 + off);
-        kv[4 * u] = x.x;
-        kv[4 * u + 1] = x.y;
-        kv[4 * u + 2] = x.z;
-        kv[4 * u + 3] = x.w;
+  for (int s = 0; s < DG; ++s)
 #pragma unroll
-        for (int t = 0; t < T; ++t) {
-          const float4 y = *reinterpret_cast<const float4*>(Kt0 + (1 + t) * Sh::TILE + off);
-          ktv[t][4 * u] = y.x;
-          ktv[t][4 * u + 1] = y.y;
-          ktv[t][4 * u + 2] = y.z;
-          ktv[t][4 * u + 3] = y.w;
-        }
-      }
-    } else {  // D = 8: two floats per lane, half a chunk
-      const int off = swz_off<D>(r, g >> 1) + (g & 1) * 8;
-      const float2 x = *reinterpret_cast<const float2*>(Kt0 + off);
-      kv[0] = x.x;
-      kv[1] = x.y;
+    for (int jt = 0; jt < NJ; ++jt) sc[jt] = mfma16x4(kv[jt][s], qf[s], sc[jt]);
 #pragma unroll
-      for (int t = 0; t < T; ++t) {
-        const float2 y = *reinterpret_cast<const float2*>(Kt0 + (1 + t) * Sh::TILE + off);
-        ktv[t][0] = y.x;
-        ktv[t][1] = y.y;
-      }
-    }
-  };
-  read_k(0, kb[0], ktb[0]);
+  for (int t = 0; t < T; ++t) {
 #pragma unroll
-  for (int jt = 0; jt < NJT; ++jt) {
-    if (jt + 1 < NJT) read_k(jt + 1, kb[(jt + 1) & 1], ktb[(jt + 1) & 1]);
-    if (jt < njt) {
-      const float* kv = kb[jt & 1];
+    for (int s = 0; s < DG; ++s)
 #pragma unroll
-      for (int s = 0; s < DG; ++s) {
-        sc[jt] = mfma16x4(kv[s], qf[s], sc[jt]);
+      for (int jt = 0; jt < NJ; ++jt) ds[t][jt] = mfma16x4(ktv[jt][t][s], qf[s], ds[t][jt]);
 #pragma unroll
-        for (int t = 0; t < T; ++t) {
-          ds[t][jt] = mfma16x4(ktb[jt & 1][t][s], qf[s], ds[t][jt]);
-          ds[t][jt] = mfma16x4(kv[s], qtf[t][s], ds[t][jt]);
-        }
-      }
-    }
+    for (int s = 0; s < DG; ++s)
+#pragma unroll
+      for (int jt = 0; jt < NJ; ++jt) ds[t][jt] = mfma16x4(kv[jt][s], qtf[t][s], ds[t][jt]);
   }
 
-  // ---- bias, validity, base-2 scores ---------------------------------------------
-  __amdgpu_buffer_rsrc_t e_rs, et_rs[TT];
-  int e_row = 0;
-  if constexpr (HAS_E) {
-    const int64_t wstride = static_cast<int64_t>(N) * N * H;
-    const int64_t ebytes = wstride * 4;
-    e_rs = make_rsrc(p.e != nullptr ? static_cast<const float*>(p.e) + b * wstride : nullptr,
-                     p.e != nullptr ? ebytes : 0);
+  // ---- V and Vt rows for the products, read while the matrix cores finish S -----------
+  const bool colok = D % 16 == 0 || c < D;
+  const int vcol = (D % 16 == 0) ? c : min(c, D - 1);
+  float va[NJ][4][DT];
+  float vta[NJ][TT][4][DT];
 #pragma unroll
-    for (int t = 0; t < T; ++t)
-      et_rs[t] = make_rsrc(p.et != nullptr ? static_cast<const float*>(p.et) + t * p.et_stride + b * wstride : nullptr,
-                           p.et != nullptr ? ebytes : 0);
-    e_row = static_cast<int>(qsite * p.e_sq + h * p.e_sh);
-  }
-  const int e_oob = static_cast<int>(static_cast<int64_t>(N) * N * H * 4);
+  for (int jt = 0; jt < NJ; ++jt)
+#pragma unroll
+    for (int r = 0; r < 4; ++r)
+#pragma unroll
+      for (int dt = 0; dt < DT; ++dt) {
+        const int col = dt * 16 + vcol;
+        const int off = swz_off<D>(jt * 16 + 4 * r + g, col >> 2) + (col & 3) * 4;
+        va[jt][r][dt] = *reinterpret_cast<const float*>(V0 + off);
+#pragma unroll
+        for (int t = 0; t < T; ++t) vta[jt][t][r][dt] = *reinterpret_cast<const float*>(V0 + (1 + t) * Sh::TILE + off);
+      }
+  compiler_fence();
+
+  // ---- bias, validity, base-2 scores --------------------------------------------------
   float mx = -INFINITY;
 #pragma unroll
-  for (int jt = 0; jt < NJT; ++jt) {
+  for (int jt = 0; jt < NJ; ++jt) {
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
       const int j = jt * 16 + 4 * r + g;
-      const bool valid = jt < njt && j < nk;
+      const bool valid = j < nk;
       float sv = sc[jt][r];
       if constexpr (HAS_E) {
-        if (jt < njt) {
-          const int ks = key_all ? j : static_cast<int>(slot_perm[j & 63]);
-          const int eo = (valid && qvalid) ? (e_row + ks * static_cast<int>(p.e_sk)) * 4 : e_oob;
-          sv += buf_load1(e_rs, eo);
+        sv += ev[jt][r];
 #pragma unroll
-          for (int t = 0; t < T; ++t) ds[t][jt][r] += buf_load1(et_rs[t], eo);
-        }
+        for (int t = 0; t < T; ++t) ds[t][jt][r] += etv[t][jt][r];
       }
       sc[jt][r] = valid ? sv * kLog2e : -INFINITY;
 #pragma unroll
@@ -488,13 +570,13 @@ __device__ __forceinline__ void pc_tile(const FwdParams& p, const char* buf, con
   if constexpr (GIVEN_LSE) {
     const float lse2 = qs.lse_in * kLog2e;
 #pragma unroll
-    for (int jt = 0; jt < NJT; ++jt)
+    for (int jt = 0; jt < NJ; ++jt)
 #pragma unroll
       for (int r = 0; r < 4; ++r) sc[jt][r] = fast_exp2(sc[jt][r] - lse2);
   } else {
     mx = group_max(mx);
 #pragma unroll
-    for (int jt = 0; jt < NJT; ++jt)
+    for (int jt = 0; jt < NJ; ++jt)
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
         sc[jt][r] = fast_exp2(sc[jt][r] - mx);
@@ -506,13 +588,15 @@ __device__ __forceinline__ void pc_tile(const FwdParams& p, const char* buf, con
   for (int t = 0; t < T; ++t) {
     mu[t] = 0.f;
 #pragma unroll
-    for (int jt = 0; jt < NJT; ++jt) {
+    for (int jt = 0; jt < NJ; ++jt) {
       ds[t][jt] *= sc[jt];
       mu[t] += (ds[t][jt][0] + ds[t][jt][1]) + (ds[t][jt][2] + ds[t][jt][3]);
     }
   }
 
-  // ---- O^T, A^T, C^T: step r of tile jt contracts keys jt*16 + 4r + (0..3) --------
+  // ---- O^T, A^T, C^T: step r of tile jt contracts keys jt*16 + 4r + (0..3); steps of
+  // the last tile whose four keys are all padding are skipped ----------------------------
+  const bool colmask = !colok;
   v4f o[DT];
   v4f at[TT][DT];
   v4f ct[TT][DT];
@@ -522,44 +606,19 @@ __device__ __forceinline__ void pc_tile(const FwdParams& p, const char* buf, con
 #pragma unroll
     for (int t = 0; t < T; ++t) at[t][dt] = ct[t][dt] = zero4();
   }
-  const bool colok = D % 16 == 0 || c < D;
-  float vb[2][4][DT];
-  float vtb[2][TT][4][DT];
-  auto read_v = [&](int jt, float (*va)[DT], float (*vta)[4][DT]) {
+#pragma unroll
+  for (int jt = 0; jt < NJ; ++jt) {
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
-      const int row = jt * 16 + 4 * r + g;
+      if (jt < NJ - 1 || r == 0 || jt * 16 + 4 * r < nk) {
 #pragma unroll
-      for (int dt = 0; dt < DT; ++dt) {
-        const int col = (D % 16 == 0) ? dt * 16 + c : min(c, D - 1);
-        const int off = swz_off<D>(row, col >> 2) + (col & 3) * 4;
-        const float x = *reinterpret_cast<const float*>(Vt0 + off);
-        va[r][dt] = colok ? x : 0.f;
+        for (int dt = 0; dt < DT; ++dt) {
+          const float vv = colmask ? 0.f : va[jt][r][dt];
+          if constexpr (!GIVEN_LSE) o[dt] = mfma16x4(vv, sc[jt][r], o[dt]);
 #pragma unroll
-        for (int t = 0; t < T; ++t) {
-          const float y = *reinterpret_cast<const float*>(Vt0 + (1 + t) * Sh::TILE + off);
-          vta[t][r][dt] = colok ? y : 0.f;
-        }
-      }
-    }
-  };
-  read_v(0, vb[0], vtb[0]);
-#pragma unroll
-  for (int jt = 0; jt < NJT; ++jt) {
-    if (jt + 1 < NJT) read_v(jt + 1, vb[(jt + 1) & 1], vtb[(jt + 1) & 1]);
-    if (jt < njt) {
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        if (jt * 16 + 4 * r < nk) {
-#pragma unroll
-          for (int dt = 0; dt < DT; ++dt) {
-            const float va = vb[jt & 1][r][dt];
-            if constexpr (!GIVEN_LSE) o[dt] = mfma16x4(va, sc[jt][r], o[dt]);
-#pragma unroll
-            for (int t = 0; t < T; ++t) {
-              at[t][dt] = mfma16x4(va, ds[t][jt][r], at[t][dt]);
-              ct[t][dt] = mfma16x4(vtb[jt & 1][t][r][dt], sc[jt][r], ct[t][dt]);
-            }
+          for (int t = 0; t < T; ++t) {
+            at[t][dt] = mfma16x4(vv, ds[t][jt][r], at[t][dt]);
+            ct[t][dt] = mfma16x4(colmask ? 0.f : vta[jt][t][r][dt], sc[jt][r], ct[t][dt]);
           }
         }
       }
@@ -575,6 +634,13 @@ __device__ __forceinline__ void pc_tile(const FwdParams& p, const char* buf, con
 #pragma unroll
   for (int t = 0; t < T; ++t) mut[t] = group_sum(mu[t]) * inv;
 
+  float ov[DT][4];
+#pragma unroll
+  for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) ov[dt][r] = GIVEN_LSE ? qs.oin[dt][r] : o[dt][r] * inv;
+  sq();
+
   // ---- stores: unconditional, invalid lanes past the walker's last record ------------
   const int64_t wrow = static_cast<int64_t>(N) * H * D;  // floats per walker
   const int obytes = static_cast<int>(wrow * 4);
@@ -585,7 +651,7 @@ __device__ __forceinline__ void pc_tile(const FwdParams& p, const char* buf, con
     for (int dt = 0; dt < DT; ++dt) {
       const int d0 = dt * 16 + 4 * g;
       const int voff = (qvalid && (D % 16 == 0 || d0 < D)) ? (obase + d0) * 4 : obytes;
-      buf_store4(o_rs, voff, o[dt][0] * inv, o[dt][1] * inv, o[dt][2] * inv, o[dt][3] * inv);
+      buf_store4(o_rs, voff, ov[dt][0], ov[dt][1], ov[dt][2], ov[dt][3]);
     }
     const int lbytes = N * H * 4;
     const __amdgpu_buffer_rsrc_t l_rs =
@@ -602,10 +668,7 @@ __device__ __forceinline__ void pc_tile(const FwdParams& p, const char* buf, con
       const int voff = (qvalid && (D % 16 == 0 || d0 < D)) ? (obase + d0) * 4 : obytes;
       float tv[4];
 #pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const float orr = GIVEN_LSE ? qs.oin[dt][r] : o[dt][r] * inv;
-        tv[r] = (at[t][dt][r] + ct[t][dt][r]) * inv - mut[t] * orr;
-      }
+      for (int r = 0; r < 4; ++r) tv[r] = (at[t][dt][r] + ct[t][dt][r]) * inv - mut[t] * ov[dt][r];
       buf_store4(t_rs, voff, tv[0], tv[1], tv[2], tv[3]);
     }
   }
@@ -634,15 +697,30 @@ __device__ __forceinline__ void pc_consumer(const FwdParams& p, const char* lds,
     }
   };
 
-  auto compute = [&](const QSet<D, T>& qs, int k) {
+  // Item k with this wave's query fragments qs; the next item's go into nq_set.
+  auto compute = [&](const QSet<D, T>& qs, QSet<D, T>& nx, int k) {
     const char* buf = lds + (k & 1) * Sh::BUF;
     const int nq = pc_nq(qs.n_phys, km, N);
-    if (wave * 16 < nq) pc_tile<D, T, GIVEN_LSE, HAS_E>(p, buf, slot_perm(k), qs, wave);
+    const int nk = pc_nk(qs.n_phys, km, N);
+    auto pf = [&]() { prefetch(nx, qs, k + 1); };
+    auto sq = [&]() { settle_q<D, T, GIVEN_LSE>(nx); };
+    const int16_t* sp = slot_perm(k);
+    if (wave * 16 < nq) {
+      switch ((nk + 15) >> 4) {
+        case 1: pc_tile<D, T, GIVEN_LSE, HAS_E, 1>(p, buf, sp, qs, wave, pf, sq); break;
+        case 2: pc_tile<D, T, GIVEN_LSE, HAS_E, 2>(p, buf, sp, qs, wave, pf, sq); break;
+        case 3: pc_tile<D, T, GIVEN_LSE, HAS_E, 3>(p, buf, sp, qs, wave, pf, sq); break;
+        default: pc_tile<D, T, GIVEN_LSE, HAS_E, 4>(p, buf, sp, qs, wave, pf, sq); break;
+      }
+    } else {
+      pf();
+      sq();
+    }
     // A fourth query tile (n > 48) goes to consumer 0, with its fragments loaded here.
     if (wave == 0 && 3 * 16 < nq) {
       QSet<D, T> q3;
-      pc_load_q<D, T, GIVEN_LSE>(p, q3, qs.b, qs.h, qs.n_phys, slot_perm(k), 3);
-      pc_tile<D, T, GIVEN_LSE, HAS_E>(p, buf, slot_perm(k), q3, 3);
+      pc_load_q<D, T, GIVEN_LSE>(p, q3, qs.b, qs.h, qs.n_phys, sp, 3);
+      pc_tile<D, T, GIVEN_LSE, HAS_E, 4>(p, buf, sp, q3, 3, [] {}, [] {});
     }
     __builtin_amdgcn_s_waitcnt(kWaitLgkm0);
   };
@@ -655,12 +733,10 @@ __device__ __forceinline__ void pc_consumer(const FwdParams& p, const char* lds,
     pc_load_q<D, T, GIVEN_LSE>(p, qa, b, h, slot_n(0), slot_perm(0), wave);
   }
   for (int k = 0; k < cnt; k += 2) {
-    prefetch(qb, qa, k + 1);
-    compute(qa, k);
+    compute(qa, qb, k);
     wg_barrier();
     if (k + 1 >= cnt) break;
-    prefetch(qa, qb, k + 2);
-    compute(qb, k + 1);
+    compute(qb, qa, k + 1);
     wg_barrier();
   }
 }
