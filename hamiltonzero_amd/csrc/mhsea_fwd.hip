@@ -482,6 +482,7 @@ hipError_t device_cu_count(int* cus) {
 hipError_t launch_fwd(const FwdParams& p, int D, int T, bool given_lse, int dtype,
                       hipStream_t stream) {
   if (!p.force_generic) {
+    if (dtype == 1 && bf16_large_fwd_supported(p.N, D)) return launch_fwd_bf16_large(p, D, T, given_lse, stream);
     if (dtype == 1 && bf16_fwd_supported(D)) return launch_fwd_bf16(p, D, T, given_lse, stream);
     if (small_fwd_supported(p.N, D, T)) return launch_fwd_small(p, D, T, given_lse, dtype, stream);
     if (pc_fwd_supported(p.N, p.H, D, T, dtype)) return launch_fwd_pc(p, D, T, given_lse, stream);

@@ -1,0 +1,515 @@
+// bfloat16 forward / forward+tangent / tangent-only MHSEA kernel for large N (N > 128,
+// D in {32, 64}), bfloat16 storage, fp32 softmax and accumulation.
+//
+// Work decomposition: one 512-thread workgroup (8 waves) owns one (walker, head) and 128
+// consecutive compacted queries; each wave owns 16 of them. Keys are streamed in chunks of
+// 64 compacted keys through a double-buffered LDS pipeline: while the waves multiply chunk
+// i from one buffer, chunk i+1 (loaded into registers during chunk i-1) is written to the
+// other buffer and chunk i+2's global reads are issued. One barrier per chunk. A chunk is
+// staged once per 128 queries (not per 64), halving the key traffic of the 4-wave kernel.
+//
+// LDS layout per buffer: K and Kt[t] row-major ([key][d], rows padded to D + 8 bf16),
+// V and Vt[t] transposed ([d][key], rows padded to 68 bf16). The transposition happens in
+// registers: a thread loads 4 consecutive keys x 8 columns (four 16-byte reads) and writes
+// 8 columns x 4 keys with v_perm_b32 and eight 8-byte LDS writes. With 68-element rows the
+// P.V operand reads (16 rows x one 8-byte run) hit 16 distinct bank pairs.
+//
+// Products run on v_mfma_f32_16x16x32_bf16 (bf16 operands, fp32 accumulation), in the
+// transposed orientation S^T = K Q^T, O^T += V^T P^T of the other kernels:
+//   S^T[key 16 jt + 4g + r][query c] = sum_s K[16 jt + c][32 s + 8g .. +8] . Q[c][32 s + 8g .. +8]
+//   O^T[d 16 dt + 4g + r][query c] += sum over key pairs (2p, 2p+1) of
+//       V^T[16 dt + c][kappa(g, i)] . P[c][kappa(g, i)],  kappa(g, i) = 16 (2p + i/4) + 4g + i%4
+// so the B operand of the P.V product is the lane's own softmax weights of two key tiles,
+// rounded to bf16.
+//
+// Online softmax with a lazy rescale: the exponent base m of a query row only moves when
+// the chunk maximum exceeds it by more than 8 (base 2), and the accumulators are rescaled
+// only then (a wave-uniform branch); weights exp2(s - m) stay <= 256, and out = O / l,
+// lse = (m + log2 l) ln 2 are exact for any base.
+#include "mhsea_device.h"
+#include "mhsea_launch.h"
+
+namespace hz {
+namespace {
+
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+
+constexpr int kWaves = 8;
+constexpr int kThreads = 64 * kWaves;
+constexpr int kQB = 16 * kWaves;  // queries per workgroup
+constexpr int kKC = 64;           // keys per chunk
+constexpr float kRescale = 8.f;   // lazy-rescale threshold (base-2 exponent)
+
+__device__ __forceinline__ v4f mfma_bf16(bf16x8 a, bf16x8 b, v4f c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+}
+__device__ __forceinline__ bf16x8 as_bf16x8(uint4 u) { return __builtin_bit_cast(bf16x8, u); }
+__device__ __forceinline__ uint4 keep4(bool keep, const uint4& u) {
+  return make_uint4(keep ? u.x : 0u, keep ? u.y : 0u, keep ? u.z : 0u, keep ? u.w : 0u);
+}
+__device__ __forceinline__ bf16x8 pack8(v4f a, v4f b) {
+  uint4 u;
+  u.x = pack2_bf16(a[0], a[1]);
+  u.y = pack2_bf16(a[2], a[3]);
+  u.z = pack2_bf16(b[0], b[1]);
+  u.w = pack2_bf16(b[2], b[3]);
+  return as_bf16x8(u);
+}
+// Word w of a uint4.
+__device__ __forceinline__ uint32_t word(const uint4& u, int w) { return w == 0 ? u.x : w == 1 ? u.y : w == 2 ? u.z : u.w; }
+
+template <int D, int T>
+struct LShape {
+  static constexpr int LDR = D + 8;   // row-major row, bf16
+  static constexpr int LDT = 68;      // transposed row (64 keys + 4), bf16
+  static constexpr int NS = D / 32;
+  static constexpr int DT = D / 16;
+  static constexpr int TT = T > 0 ? T : 1;
+  static constexpr int C8 = D / 8;    // 16-byte chunks of a row
+  static constexpr int NX = 1 + T;    // tensors of each kind (K-like, V-like)
+  static constexpr int kRow = kKC * LDR;  // elements of one row-major tile
+  static constexpr int kTr = D * LDT;     // elements of one transposed tile
+  static constexpr int kBuf = NX * (kRow + kTr);  // elements of one buffer
+  // Staging work per chunk: K-like 16-byte items, V-like 4-key x 8-column units.
+  static constexpr int kKItems = NX * kKC * C8;
+  static constexpr int kKPer = (kKItems + kThreads - 1) / kThreads;
+  static constexpr int kVUnits = NX * (kKC / 4) * C8;
+  static constexpr int kVPer = (kVUnits + kThreads - 1) / kThreads;
+  static size_t lds_bytes(int N) {
+    const size_t n16 = (static_cast<size_t>(N) + 15) & ~size_t(15);
+    return static_cast<size_t>(2 * kBuf) * 2 + 64 + n16 + 2 * n16;
+  }
+};
+
+// Mask compaction for a workgroup of kWaves waves: idx[0..count) = physical sites
+// (ascending), mask_s = the raw mask bytes. Returns count to every thread.
+__device__ __forceinline__ int compact_mask_wg(const uint8_t* __restrict__ mask_row, int N, int16_t* __restrict__ idx,
+                                               uint8_t* __restrict__ mask_s, int* __restrict__ scratch) {
+  const int tid = threadIdx.x;
+  const int wave = tid >> 6;
+  const int lane = tid & 63;
+  int total = 0;
+  for (int base = 0; base < N; base += kThreads) {
+    const int pos = base + tid;
+    const uint8_t m = pos < N ? mask_row[pos] : 0;
+    if (pos < N) mask_s[pos] = m;
+    const bool on = m != 0;
+    const uint64_t bal = __ballot(on);
+    if (lane == 0) scratch[wave] = __popcll(bal);
+    __syncthreads();
+    int before = total;
+    for (int w = 0; w < wave; ++w) before += scratch[w];
+    if (on) idx[before + __popcll(bal & ((uint64_t(1) << lane) - 1))] = static_cast<int16_t>(pos);
+    for (int w = 0; w < kWaves; ++w) total += scratch[w];
+    __syncthreads();
+  }
+  return total;
+}
+
+template <int D, int T, bool GIVEN_LSE, bool HAS_E>
+__global__ void __launch_bounds__(kThreads, 1) mhsea_fwd_bf16_large_kernel(const FwdParams p) {
+  using Sh = LShape<D, T>;
+  constexpr int LDR = Sh::LDR, LDT = Sh::LDT, NS = Sh::NS, DT = Sh::DT, TT = Sh::TT, C8 = Sh::C8, NX = Sh::NX;
+  constexpr int NJT = kKC / 16;
+
+  extern __shared__ float4 smem4[];
+  uint16_t* const lds = reinterpret_cast<uint16_t*>(smem4);
+  int* const scratch = reinterpret_cast<int*>(lds + 2 * Sh::kBuf);
+  const int n16 = (p.N + 15) & ~15;
+  uint8_t* const mask_s = reinterpret_cast<uint8_t*>(scratch + 16);
+  int16_t* const idx = reinterpret_cast<int16_t*>(mask_s + n16);
+
+  const int N = p.N, H = p.H;
+  const int nblk = (N + kQB - 1) / kQB;
+  const int64_t nwg = static_cast<int64_t>(p.B) * H * nblk;
+  const int64_t lb = xcd_logical_block(blockIdx.x, nwg);
+  const int blk = static_cast<int>(lb % nblk);
+  const int h = static_cast<int>((lb / nblk) % H);
+  const int b = static_cast<int>(lb / (static_cast<int64_t>(nblk) * H));
+
+  const int tid = threadIdx.x;
+  const int wave = tid >> 6;
+  const int lane = tid & 63;
+  const int g = lane >> 4;
+  const int c = lane & 15;
+
+  const int n_phys = compact_mask_wg(p.mask + static_cast<int64_t>(b) * N, N, idx, mask_s, scratch);
+  const bool key_all = p.key_mask && n_phys == 0;
+  const int nk = key_all ? N : n_phys;
+  const int nq = p.key_mask ? N : n_phys;
+  const int nchunks = (nk + kKC - 1) / kKC;
+
+  // Tensor x of each kind: 0 = primal, 1..T = tangent x-1. A null tangent reads the
+  // primal and is zeroed.
+  auto ksrc = [&](int x) -> const uint16_t* {
+    if (x == 0) return static_cast<const uint16_t*>(p.k);
+    return p.kt != nullptr ? static_cast<const uint16_t*>(p.kt) + (x - 1) * p.t_stride
+                           : static_cast<const uint16_t*>(p.k);
+  };
+  auto vsrc = [&](int x) -> const uint16_t* {
+    if (x == 0) return static_cast<const uint16_t*>(p.v);
+    return p.vt != nullptr ? static_cast<const uint16_t*>(p.vt) + (x - 1) * p.t_stride
+                           : static_cast<const uint16_t*>(p.v);
+  };
+  auto kkeep = [&](int x) { return x == 0 || p.kt != nullptr; };
+  auto vkeep = [&](int x) { return x == 0 || p.vt != nullptr; };
+  auto site_of = [&](int j) { return key_all ? j : static_cast<int>(idx[j]); };
+
+  // ---- chunk staging: global -> registers (load), registers -> LDS buffer (store) -----
+  uint4 rk[Sh::kKPer];
+  uint4 rv[Sh::kVPer][4];
+  auto chunk_load = [&](int kc) {
+#pragma unroll
+    for (int u = 0; u < Sh::kKPer; ++u) {
+      const int it = tid + u * kThreads;
+      const int x = it / (kKC * C8);
+      const int rem = it % (kKC * C8);
+      const int r = rem / C8;
+      const bool ok = (Sh::kKItems % kThreads == 0 || it < Sh::kKItems) && kc + r < nk;
+      const int site = ok ? site_of(kc + r) : 0;
+      const int xx = (Sh::kKItems % kThreads == 0 || it < Sh::kKItems) ? x : 0;
+      rk[u] = *reinterpret_cast<const uint4*>(ksrc(xx) + bnhd(b, site, h, N, H, D) + (rem % C8) * 8);
+    }
+#pragma unroll
+    for (int u = 0; u < Sh::kVPer; ++u) {
+      const int it = tid + u * kThreads;
+      const bool unit_ok = Sh::kVUnits % kThreads == 0 || it < Sh::kVUnits;
+      const int x = unit_ok ? it / ((kKC / 4) * C8) : 0;
+      const int rem = it % ((kKC / 4) * C8);
+      const int kg = rem % (kKC / 4), dg = rem / (kKC / 4);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int j = kc + 4 * kg + i;
+        const int site = (unit_ok && j < nk) ? site_of(j) : 0;
+        rv[u][i] = *reinterpret_cast<const uint4*>(vsrc(x) + bnhd(b, site, h, N, H, D) + dg * 8);
+      }
+    }
+  };
+  auto chunk_store = [&](int kc, int buf) {
+    uint16_t* const base = lds + buf * Sh::kBuf;
+#pragma unroll
+    for (int u = 0; u < Sh::kKPer; ++u) {
+      const int it = tid + u * kThreads;
+      if (Sh::kKItems % kThreads == 0 || it < Sh::kKItems) {
+        const int x = it / (kKC * C8);
+        const int rem = it % (kKC * C8);
+        const int r = rem / C8;
+        *reinterpret_cast<uint4*>(base + x * Sh::kRow + r * LDR + (rem % C8) * 8) =
+            keep4(kc + r < nk && kkeep(x), rk[u]);
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < Sh::kVPer; ++u) {
+      const int it = tid + u * kThreads;
+      if (Sh::kVUnits % kThreads == 0 || it < Sh::kVUnits) {
+        const int x = it / ((kKC / 4) * C8);
+        const int rem = it % ((kKC / 4) * C8);
+        const int kg = rem % (kKC / 4), dg = rem / (kKC / 4);
+        uint4 v4[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) v4[i] = keep4(kc + 4 * kg + i < nk && vkeep(x), rv[u][i]);
+        uint16_t* const tr = base + NX * Sh::kRow + x * Sh::kTr + (dg * 8) * LDT + 4 * kg;
+#pragma unroll
+        for (int w = 0; w < 4; ++w) {
+          // columns 2w (low halves) and 2w + 1 (high halves) of the four keys
+          uint2 ev, od;
+          ev.x = __builtin_amdgcn_perm(word(v4[1], w), word(v4[0], w), 0x05040100u);
+          ev.y = __builtin_amdgcn_perm(word(v4[3], w), word(v4[2], w), 0x05040100u);
+          od.x = __builtin_amdgcn_perm(word(v4[1], w), word(v4[0], w), 0x07060302u);
+          od.y = __builtin_amdgcn_perm(word(v4[3], w), word(v4[2], w), 0x07060302u);
+          *reinterpret_cast<uint2*>(tr + (2 * w) * LDT) = ev;
+          *reinterpret_cast<uint2*>(tr + (2 * w + 1) * LDT) = od;
+        }
+      }
+    }
+  };
+
+  // ---- this wave's queries -------------------------------------------------------------
+  const int q0 = blk * kQB + wave * 16;
+  const bool active = q0 < nq;
+  const bool qvalid = q0 + c < nq;
+  const int qsite = qvalid ? (p.key_mask ? (q0 + c) : idx[q0 + c]) : -1;
+  const int qload = qvalid ? qsite : 0;
+  bf16x8 qf[NS], qtf[TT][NS];
+  {
+    const int64_t qoff = bnhd(b, qload, h, N, H, D) + 8 * g;
+    const uint16_t* qt = p.qt != nullptr ? static_cast<const uint16_t*>(p.qt) : static_cast<const uint16_t*>(p.q);
+    const int64_t qts = p.qt != nullptr ? p.t_stride : 0;
+#pragma unroll
+    for (int s = 0; s < NS; ++s) {
+      qf[s] = as_bf16x8(*reinterpret_cast<const uint4*>(static_cast<const uint16_t*>(p.q) + qoff + 32 * s));
+#pragma unroll
+      for (int t = 0; t < T; ++t)
+        qtf[t][s] = as_bf16x8(*reinterpret_cast<const uint4*>(qt + t * qts + qoff + 32 * s));
+    }
+  }
+  const float sscale = p.scale;
+  const float stscale = p.qt != nullptr ? p.scale : 0.f;
+  float lse2 = 0.f;
+  if constexpr (GIVEN_LSE) lse2 = p.lse_in[(static_cast<int64_t>(b) * N + qload) * H + h] * kLog2e;
+  const int64_t e_row = static_cast<int64_t>(b) * N * N * H + static_cast<int64_t>(qload) * p.e_sq +
+                        static_cast<int64_t>(h) * p.e_sh;
+
+  v4f o[DT], at[TT][DT], ct[TT][DT];
+#pragma unroll
+  for (int dt = 0; dt < DT; ++dt) {
+    o[dt] = zero4();
+#pragma unroll
+    for (int t = 0; t < T; ++t) at[t][dt] = ct[t][dt] = zero4();
+  }
+  float m2 = -INFINITY, lsum = 0.f;
+  float mu[TT];
+#pragma unroll
+  for (int t = 0; t < T; ++t) mu[t] = 0.f;
+
+  // ---- pipeline prologue -----------------------------------------------------------------
+  if (nchunks > 0) {
+    chunk_load(0);
+    chunk_store(0, 0);
+    if (nchunks > 1) chunk_load(kKC);
+  }
+  __syncthreads();
+
+  for (int ch = 0; ch < nchunks; ++ch) {
+    const int kc = ch * kKC;
+    const uint16_t* const Kb = lds + (ch & 1) * Sh::kBuf;
+    const uint16_t* const Vb = Kb + NX * Sh::kRow;
+    // stage chunk ch+1 (in registers since chunk ch-1) into the other buffer, then start
+    // the reads of chunk ch+2
+    if (ch + 1 < nchunks) {
+      chunk_store(kc + kKC, (ch + 1) & 1);
+      if (ch + 2 < nchunks) chunk_load(kc + 2 * kKC);
+    }
+
+    if (active) {
+      const int jn = min(kKC, nk - kc);
+      const int njt = (jn + 15) >> 4;
+      v4f sc[NJT], ds[TT][NJT];
+#pragma unroll
+      for (int jt = 0; jt < NJT; ++jt) {
+        sc[jt] = zero4();
+#pragma unroll
+        for (int t = 0; t < T; ++t) ds[t][jt] = zero4();
+        if (jt < njt) {
+          const uint16_t* krow = Kb + (jt * 16 + c) * LDR + 8 * g;
+#pragma unroll
+          for (int s = 0; s < NS; ++s) {
+            const bf16x8 kv = as_bf16x8(*reinterpret_cast<const uint4*>(krow + 32 * s));
+            sc[jt] = mfma_bf16(kv, qf[s], sc[jt]);
+#pragma unroll
+            for (int t = 0; t < T; ++t) {
+              const bf16x8 ktv = as_bf16x8(*reinterpret_cast<const uint4*>(krow + (1 + t) * Sh::kRow + 32 * s));
+              ds[t][jt] = mfma_bf16(ktv, qf[s], ds[t][jt]);
+              ds[t][jt] = mfma_bf16(kv, qtf[t][s], ds[t][jt]);
+            }
+          }
+        }
+      }
+
+      float mx = -INFINITY;
+#pragma unroll
+      for (int jt = 0; jt < NJT; ++jt) {
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int j = kc + jt * 16 + 4 * g + r;
+          const bool valid = jt < njt && j < nk;
+          float sv = sc[jt][r] * sscale;
+#pragma unroll
+          for (int t = 0; t < T; ++t) ds[t][jt][r] *= stscale;
+          if constexpr (HAS_E) {
+            if (valid) {
+              const int64_t eo = e_row + static_cast<int64_t>(site_of(j)) * p.e_sk;
+              if (p.e != nullptr) sv += load1<BF16>(p.e, eo);
+              if (p.et != nullptr) {
+#pragma unroll
+                for (int t = 0; t < T; ++t) ds[t][jt][r] += load1<BF16>(p.et, t * p.et_stride + eo);
+              }
+            }
+          }
+          sc[jt][r] = valid ? sv * kLog2e : -INFINITY;
+#pragma unroll
+          for (int t = 0; t < T; ++t) ds[t][jt][r] = valid ? ds[t][jt][r] : 0.f;
+          mx = fmaxf(mx, sc[jt][r]);
+        }
+      }
+
+      if constexpr (GIVEN_LSE) {
+#pragma unroll
+        for (int jt = 0; jt < NJT; ++jt)
+#pragma unroll
+          for (int r = 0; r < 4; ++r) sc[jt][r] = fast_exp2(sc[jt][r] - lse2);
+      } else {
+        mx = group_max(mx);
+        const bool need = mx > m2 + kRescale;  // also true for the first chunk (m2 = -inf)
+        if (__any(need)) {
+          const float mnew = need ? mx : m2;
+          const float alpha = fast_exp2(m2 - mnew);  // 1 where unchanged, 0 on the first chunk
+          lsum *= alpha;
+#pragma unroll
+          for (int dt = 0; dt < DT; ++dt) {
+            o[dt] *= alpha;
+#pragma unroll
+            for (int t = 0; t < T; ++t) {
+              at[t][dt] *= alpha;
+              ct[t][dt] *= alpha;
+            }
+          }
+#pragma unroll
+          for (int t = 0; t < T; ++t) mu[t] *= alpha;
+          m2 = mnew;
+        }
+#pragma unroll
+        for (int jt = 0; jt < NJT; ++jt)
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            sc[jt][r] = fast_exp2(sc[jt][r] - m2);
+            lsum += sc[jt][r];
+          }
+      }
+#pragma unroll
+      for (int t = 0; t < T; ++t)
+#pragma unroll
+        for (int jt = 0; jt < NJT; ++jt) {
+          ds[t][jt] *= sc[jt];
+          mu[t] += (ds[t][jt][0] + ds[t][jt][1]) + (ds[t][jt][2] + ds[t][jt][3]);
+        }
+
+      // ---- P.V products over key pairs ------------------------------------------------
+#pragma unroll
+      for (int pp = 0; pp < NJT / 2; ++pp) {
+        if (2 * pp < njt) {
+          const bf16x8 pw = pack8(sc[2 * pp], sc[2 * pp + 1]);
+          bf16x8 pdw[TT];
+#pragma unroll
+          for (int t = 0; t < T; ++t) pdw[t] = pack8(ds[t][2 * pp], ds[t][2 * pp + 1]);
+#pragma unroll
+          for (int dt = 0; dt < DT; ++dt) {
+            const uint16_t* vrow = Vb + (dt * 16 + c) * LDT + pp * 32 + 4 * g;
+            const uint2 lo = *reinterpret_cast<const uint2*>(vrow);
+            const uint2 hi = *reinterpret_cast<const uint2*>(vrow + 16);
+            const bf16x8 vv = as_bf16x8(make_uint4(lo.x, lo.y, hi.x, hi.y));
+            if constexpr (!GIVEN_LSE) o[dt] = mfma_bf16(vv, pw, o[dt]);
+#pragma unroll
+            for (int t = 0; t < T; ++t) {
+              at[t][dt] = mfma_bf16(vv, pdw[t], at[t][dt]);
+              const uint16_t* trow = vrow + (1 + t) * Sh::kTr;
+              const uint2 tl = *reinterpret_cast<const uint2*>(trow);
+              const uint2 th = *reinterpret_cast<const uint2*>(trow + 16);
+              ct[t][dt] = mfma_bf16(as_bf16x8(make_uint4(tl.x, tl.y, th.x, th.y)), pw, ct[t][dt]);
+            }
+          }
+        }
+      }
+    }
+    __syncthreads();
+  }
+
+  if (active) {
+    float inv = 1.f, l2tot = 0.f;
+    if constexpr (!GIVEN_LSE) {
+      l2tot = group_sum(lsum);
+      inv = 1.f / l2tot;
+    }
+    float mut[TT];
+#pragma unroll
+    for (int t = 0; t < T; ++t) mut[t] = group_sum(mu[t]) * inv;
+    if (qvalid) {
+      const int64_t obase = bnhd(b, qsite, h, N, H, D);
+#pragma unroll
+      for (int dt = 0; dt < DT; ++dt) {
+        const int d0 = dt * 16 + 4 * g;
+        float o4[4];
+        if constexpr (!GIVEN_LSE) {
+#pragma unroll
+          for (int r = 0; r < 4; ++r) o4[r] = o[dt][r] * inv;
+          store4<BF16>(p.out, obase + d0, o4[0], o4[1], o4[2], o4[3]);
+        } else {
+          const float4 x = load4<BF16>(p.out_in, obase + d0);
+          o4[0] = x.x;
+          o4[1] = x.y;
+          o4[2] = x.z;
+          o4[3] = x.w;
+        }
+#pragma unroll
+        for (int t = 0; t < T; ++t) {
+          float tv[4];
+#pragma unroll
+          for (int r = 0; r < 4; ++r) tv[r] = (at[t][dt][r] + ct[t][dt][r]) * inv - mut[t] * o4[r];
+          store4<BF16>(p.tout, t * p.t_stride + obase + d0, tv[0], tv[1], tv[2], tv[3]);
+        }
+      }
+      if constexpr (!GIVEN_LSE) {
+        if (g == 0 && p.lse != nullptr)
+          p.lse[(static_cast<int64_t>(b) * N + qsite) * H + h] = (m2 + log2f(l2tot)) * kLn2;
+      }
+    }
+  }
+
+  // rows of masked sites in this block's site range (square mask): zeros, lse = -1e4 + log N
+  if (!p.key_mask) {
+    constexpr int C4 = D / 4;
+    const int r0 = blk * kQB;
+    for (int it = tid; it < kQB * C4; it += kThreads) {
+      const int r = r0 + it / C4;
+      const int c4 = it % C4;
+      if (r < N && mask_s[r] == 0) {
+        const int64_t off = bnhd(b, r, h, N, H, D) + c4 * 4;
+        if constexpr (!GIVEN_LSE) store4<BF16>(p.out, off, 0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+        for (int t = 0; t < T; ++t) store4<BF16>(p.tout, t * p.t_stride + off, 0.f, 0.f, 0.f, 0.f);
+        if (!GIVEN_LSE && c4 == 0 && p.lse != nullptr)
+          p.lse[(static_cast<int64_t>(b) * N + r) * H + h] = p.masked_lse;
+      }
+    }
+  }
+}
+
+template <int D, int T, bool GIVEN_LSE, bool HAS_E>
+hipError_t launch_t(const FwdParams& p, hipStream_t stream) {
+  using Sh = LShape<D, T>;
+  const int nblk = (p.N + kQB - 1) / kQB;
+  const int64_t nwg = static_cast<int64_t>(p.B) * p.H * nblk;
+  const size_t lds = Sh::lds_bytes(p.N);
+  auto kern = mhsea_fwd_bf16_large_kernel<D, T, GIVEN_LSE, HAS_E>;
+  if (lds > 64 * 1024) {
+    hipError_t err = hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
+                                         hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(lds));
+    if (err != hipSuccess) return err;
+  }
+  hipLaunchKernelGGL(kern, dim3(static_cast<unsigned>(nwg)), dim3(kThreads), lds, stream, p);
+  return hipGetLastError();
+}
+
+template <int D, int T, bool GIVEN_LSE>
+hipError_t dispatch_e(const FwdParams& p, hipStream_t stream) {
+  if (p.e != nullptr || p.et != nullptr) return launch_t<D, T, GIVEN_LSE, true>(p, stream);
+  return launch_t<D, T, GIVEN_LSE, false>(p, stream);
+}
+
+template <int D>
+hipError_t dispatch_t(const FwdParams& p, int T, bool given_lse, hipStream_t stream) {
+  if (given_lse) {
+    if (T == 1) return dispatch_e<D, 1, true>(p, stream);
+    if (T == 2) return dispatch_e<D, 2, true>(p, stream);
+    return hipErrorInvalidValue;
+  }
+  if (T == 0) return dispatch_e<D, 0, false>(p, stream);
+  if (T == 1) return dispatch_e<D, 1, false>(p, stream);
+  if (T == 2) return dispatch_e<D, 2, false>(p, stream);
+  return hipErrorInvalidValue;
+}
+
+}  // namespace
+
+bool bf16_large_fwd_supported(int N, int D) {
+  // LDS: two buffers plus the walker's mask and site list must fit 160 KiB.
+  return N > 128 && (D == 32 || D == 64) && (D == 32 ? LShape<32, 2>::lds_bytes(N) : LShape<64, 2>::lds_bytes(N)) <= 160 * 1024;
+}
+
+hipError_t launch_fwd_bf16_large(const FwdParams& p, int D, int T, bool given_lse, hipStream_t stream) {
+  if (D == 32) return dispatch_t<32>(p, T, given_lse, stream);
+  if (D == 64) return dispatch_t<64>(p, T, given_lse, stream);
+  return hipErrorInvalidValue;
+}
+
+}  // namespace hz

@@ -78,6 +78,9 @@ hipError_t launch_fwd_stream(const FwdParams& p, int D, int T, bool given_lse, i
 bool stream_bwd_supported(int N);
 hipError_t launch_bwd_stream(const BwdParams& p, int D, int dtype, hipStream_t stream);
 bool bf16_fwd_supported(int D);
+// Large-N bfloat16 kernel (N > 128): 128-query workgroups, double-buffered LDS key chunks.
+bool bf16_large_fwd_supported(int N, int D);
+hipError_t launch_fwd_bf16_large(const FwdParams& p, int D, int T, bool given_lse, hipStream_t stream);
 bool bf16_bwd_supported(int N, int D);
 hipError_t launch_bwd_bf16(const BwdParams& p, int D, hipStream_t stream);
 hipError_t launch_fwd_bf16(const FwdParams& p, int D, int T, bool given_lse, hipStream_t stream);
