@@ -44,9 +44,6 @@ __device__ __forceinline__ v4f mfma_bf16(bf16x8 a, bf16x8 b, v4f c) {
   return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
 }
 __device__ __forceinline__ bf16x8 as_bf16x8(uint4 u) { return __builtin_bit_cast(bf16x8, u); }
-__device__ __forceinline__ uint4 keep4(bool keep, const uint4& u) {
-  return make_uint4(keep ? u.x : 0u, keep ? u.y : 0u, keep ? u.z : 0u, keep ? u.w : 0u);
-}
 __device__ __forceinline__ bf16x8 pack8(v4f a, v4f b) {
   uint4 u;
   u.x = pack2_bf16(a[0], a[1]);
@@ -139,21 +136,39 @@ __global__ void __launch_bounds__(kThreads, 1) mhsea_fwd_bf16_large_kernel(const
   const int nq = p.key_mask ? N : n_phys;
   const int nchunks = (nk + kKC - 1) / kKC;
 
-  // Tensor x of each kind: 0 = primal, 1..T = tangent x-1. A null tangent reads the
-  // primal and is zeroed.
-  auto ksrc = [&](int x) -> const uint16_t* {
-    if (x == 0) return static_cast<const uint16_t*>(p.k);
-    return p.kt != nullptr ? static_cast<const uint16_t*>(p.kt) + (x - 1) * p.t_stride
-                           : static_cast<const uint16_t*>(p.k);
+  // Staging reads go through buffer resources over the walker's slice of each tensor: a
+  // 32-bit byte offset per key row, zeros for padding keys (offsets past the last record)
+  // and for a null tangent (an empty resource).
+  const int64_t wel = static_cast<int64_t>(N) * H * D;  // elements per walker slice
+  const int wbytes = static_cast<int>(wel * 2);
+  auto rsrc = [&](const void* base, int64_t eoff, bool ok) {
+    return __builtin_amdgcn_make_buffer_rsrc(
+        ok ? const_cast<uint16_t*>(static_cast<const uint16_t*>(base) + eoff) : nullptr, static_cast<short>(0),
+        ok ? wbytes : 0, 0x00020000);
   };
-  auto vsrc = [&](int x) -> const uint16_t* {
-    if (x == 0) return static_cast<const uint16_t*>(p.v);
-    return p.vt != nullptr ? static_cast<const uint16_t*>(p.vt) + (x - 1) * p.t_stride
-                           : static_cast<const uint16_t*>(p.v);
+  __amdgpu_buffer_rsrc_t kr[NX], vr[NX];
+#pragma unroll
+  for (int x = 0; x < NX; ++x) {
+    const int64_t woff = b * wel + (x > 0 ? (x - 1) * p.t_stride : 0);
+    kr[x] = rsrc(x == 0 ? p.k : p.kt, woff, x == 0 || p.kt != nullptr);
+    vr[x] = rsrc(x == 0 ? p.v : p.vt, woff, x == 0 || p.vt != nullptr);
+  }
+  // resource x of an array, x wave-uniform (scalar selects, no waterfall over lanes)
+  auto pick = [&](const __amdgpu_buffer_rsrc_t* r, int x) -> __amdgpu_buffer_rsrc_t {
+    if constexpr (NX == 1) return r[0];
+    if constexpr (NX == 2) return x == 0 ? r[0] : r[1];
+    return x == 0 ? r[0] : (x == 1 ? r[1] : r[2]);
   };
-  auto kkeep = [&](int x) { return x == 0 || p.kt != nullptr; };
-  auto vkeep = [&](int x) { return x == 0 || p.vt != nullptr; };
+  const int rowstride = H * D * 2;  // bytes between sites
+  const int hoff = h * D * 2;
+  // byte offset of key j's row (padding keys: past the last record)
+  auto key_off = [&](int j) { return j < nk ? (key_all ? j : static_cast<int>(idx[j])) * rowstride + hoff : wbytes; };
   auto site_of = [&](int j) { return key_all ? j : static_cast<int>(idx[j]); };
+  auto bload = [&](const __amdgpu_buffer_rsrc_t& r, int off) -> uint4 {
+    typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
+    const u32x4_t u = __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0);
+    return make_uint4(u.x, u.y, u.z, u.w);
+  };
 
   // ---- chunk staging: global -> registers (load), registers -> LDS buffer (store) -----
   uint4 rk[Sh::kKPer];
@@ -162,30 +177,29 @@ __global__ void __launch_bounds__(kThreads, 1) mhsea_fwd_bf16_large_kernel(const
 #pragma unroll
     for (int u = 0; u < Sh::kKPer; ++u) {
       const int it = tid + u * kThreads;
-      const int x = it / (kKC * C8);
+      const bool item_ok = Sh::kKItems % kThreads == 0 || it < Sh::kKItems;
+      // the tensor of an item is uniform across a wave (64 | kKC * C8): a scalar index
+      const int x = __builtin_amdgcn_readfirstlane(item_ok ? it / (kKC * C8) : 0);
       const int rem = it % (kKC * C8);
-      const int r = rem / C8;
-      const bool ok = (Sh::kKItems % kThreads == 0 || it < Sh::kKItems) && kc + r < nk;
-      const int site = ok ? site_of(kc + r) : 0;
-      const int xx = (Sh::kKItems % kThreads == 0 || it < Sh::kKItems) ? x : 0;
-      rk[u] = *reinterpret_cast<const uint4*>(ksrc(xx) + bnhd(b, site, h, N, H, D) + (rem % C8) * 8);
+      const int off = key_off(kc + rem / C8);
+      rk[u] = bload(pick(kr, x), off == wbytes ? off : off + (rem % C8) * 16);
     }
 #pragma unroll
     for (int u = 0; u < Sh::kVPer; ++u) {
       const int it = tid + u * kThreads;
       const bool unit_ok = Sh::kVUnits % kThreads == 0 || it < Sh::kVUnits;
-      const int x = unit_ok ? it / ((kKC / 4) * C8) : 0;
+      // uniform across a wave (64 | (kKC / 4) * C8)
+      const int x = __builtin_amdgcn_readfirstlane(unit_ok ? it / ((kKC / 4) * C8) : 0);
       const int rem = it % ((kKC / 4) * C8);
       const int kg = rem % (kKC / 4), dg = rem / (kKC / 4);
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        const int j = kc + 4 * kg + i;
-        const int site = (unit_ok && j < nk) ? site_of(j) : 0;
-        rv[u][i] = *reinterpret_cast<const uint4*>(vsrc(x) + bnhd(b, site, h, N, H, D) + dg * 8);
+        const int off = key_off(kc + 4 * kg + i);
+        rv[u][i] = bload(pick(vr, x), off == wbytes ? off : off + dg * 16);
       }
     }
   };
-  auto chunk_store = [&](int kc, int buf) {
+  auto chunk_store = [&](int buf) {
     uint16_t* const base = lds + buf * Sh::kBuf;
 #pragma unroll
     for (int u = 0; u < Sh::kKPer; ++u) {
@@ -193,9 +207,7 @@ __global__ void __launch_bounds__(kThreads, 1) mhsea_fwd_bf16_large_kernel(const
       if (Sh::kKItems % kThreads == 0 || it < Sh::kKItems) {
         const int x = it / (kKC * C8);
         const int rem = it % (kKC * C8);
-        const int r = rem / C8;
-        *reinterpret_cast<uint4*>(base + x * Sh::kRow + r * LDR + (rem % C8) * 8) =
-            keep4(kc + r < nk && kkeep(x), rk[u]);
+        *reinterpret_cast<uint4*>(base + x * Sh::kRow + (rem / C8) * LDR + (rem % C8) * 8) = rk[u];
       }
     }
 #pragma unroll
@@ -205,18 +217,15 @@ __global__ void __launch_bounds__(kThreads, 1) mhsea_fwd_bf16_large_kernel(const
         const int x = it / ((kKC / 4) * C8);
         const int rem = it % ((kKC / 4) * C8);
         const int kg = rem % (kKC / 4), dg = rem / (kKC / 4);
-        uint4 v4[4];
-#pragma unroll
-        for (int i = 0; i < 4; ++i) v4[i] = keep4(kc + 4 * kg + i < nk && vkeep(x), rv[u][i]);
         uint16_t* const tr = base + NX * Sh::kRow + x * Sh::kTr + (dg * 8) * LDT + 4 * kg;
 #pragma unroll
         for (int w = 0; w < 4; ++w) {
           // columns 2w (low halves) and 2w + 1 (high halves) of the four keys
           uint2 ev, od;
-          ev.x = __builtin_amdgcn_perm(word(v4[1], w), word(v4[0], w), 0x05040100u);
-          ev.y = __builtin_amdgcn_perm(word(v4[3], w), word(v4[2], w), 0x05040100u);
-          od.x = __builtin_amdgcn_perm(word(v4[1], w), word(v4[0], w), 0x07060302u);
-          od.y = __builtin_amdgcn_perm(word(v4[3], w), word(v4[2], w), 0x07060302u);
+          ev.x = __builtin_amdgcn_perm(word(rv[u][1], w), word(rv[u][0], w), 0x05040100u);
+          ev.y = __builtin_amdgcn_perm(word(rv[u][3], w), word(rv[u][2], w), 0x05040100u);
+          od.x = __builtin_amdgcn_perm(word(rv[u][1], w), word(rv[u][0], w), 0x07060302u);
+          od.y = __builtin_amdgcn_perm(word(rv[u][3], w), word(rv[u][2], w), 0x07060302u);
           *reinterpret_cast<uint2*>(tr + (2 * w) * LDT) = ev;
           *reinterpret_cast<uint2*>(tr + (2 * w + 1) * LDT) = od;
         }
@@ -245,6 +254,7 @@ __global__ void __launch_bounds__(kThreads, 1) mhsea_fwd_bf16_large_kernel(const
   }
   const float sscale = p.scale;
   const float stscale = p.qt != nullptr ? p.scale : 0.f;
+  const float s2scale = sscale * kLog2e;
   float lse2 = 0.f;
   if constexpr (GIVEN_LSE) lse2 = p.lse_in[(static_cast<int64_t>(b) * N + qload) * H + h] * kLog2e;
   const int64_t e_row = static_cast<int64_t>(b) * N * N * H + static_cast<int64_t>(qload) * p.e_sq +
@@ -265,7 +275,7 @@ __global__ void __launch_bounds__(kThreads, 1) mhsea_fwd_bf16_large_kernel(const
   // ---- pipeline prologue -----------------------------------------------------------------
   if (nchunks > 0) {
     chunk_load(0);
-    chunk_store(0, 0);
+    chunk_store(0);
     if (nchunks > 1) chunk_load(kKC);
   }
   __syncthreads();
@@ -277,7 +287,7 @@ __global__ void __launch_bounds__(kThreads, 1) mhsea_fwd_bf16_large_kernel(const
     // stage chunk ch+1 (in registers since chunk ch-1) into the other buffer, then start
     // the reads of chunk ch+2
     if (ch + 1 < nchunks) {
-      chunk_store(kc + kKC, (ch + 1) & 1);
+      chunk_store((ch + 1) & 1);
       if (ch + 2 < nchunks) chunk_load(kc + 2 * kKC);
     }
 
@@ -306,30 +316,48 @@ __global__ void __launch_bounds__(kThreads, 1) mhsea_fwd_bf16_large_kernel(const
         }
       }
 
+      // Base-2 scores. A full chunk (every key physical) needs no validity selects. Without
+      // a bias the tangent scores stay unscaled here: P o dS is linear in the scale, which
+      // is applied once to A and mu at the end.
       float mx = -INFINITY;
+      const bool full = kc + kKC <= nk;
+      if (!HAS_E && full) {
 #pragma unroll
-      for (int jt = 0; jt < NJT; ++jt) {
+        for (int jt = 0; jt < NJT; ++jt)
 #pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          const int j = kc + jt * 16 + 4 * g + r;
-          const bool valid = jt < njt && j < nk;
-          float sv = sc[jt][r] * sscale;
-#pragma unroll
-          for (int t = 0; t < T; ++t) ds[t][jt][r] *= stscale;
-          if constexpr (HAS_E) {
-            if (valid) {
-              const int64_t eo = e_row + static_cast<int64_t>(site_of(j)) * p.e_sk;
-              if (p.e != nullptr) sv += load1<BF16>(p.e, eo);
-              if (p.et != nullptr) {
-#pragma unroll
-                for (int t = 0; t < T; ++t) ds[t][jt][r] += load1<BF16>(p.et, t * p.et_stride + eo);
-              }
-            }
+          for (int r = 0; r < 4; ++r) {
+            sc[jt][r] *= s2scale;
+            mx = fmaxf(mx, sc[jt][r]);
           }
-          sc[jt][r] = valid ? sv * kLog2e : -INFINITY;
+      } else {
 #pragma unroll
-          for (int t = 0; t < T; ++t) ds[t][jt][r] = valid ? ds[t][jt][r] : 0.f;
-          mx = fmaxf(mx, sc[jt][r]);
+        for (int jt = 0; jt < NJT; ++jt) {
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            const int j = kc + jt * 16 + 4 * g + r;
+            const bool valid = jt < njt && j < nk;
+            float sv = sc[jt][r];
+            if constexpr (HAS_E) {
+              sv *= sscale;
+#pragma unroll
+              for (int t = 0; t < T; ++t) ds[t][jt][r] *= stscale;
+              if (valid) {
+                const int64_t eo = e_row + static_cast<int64_t>(site_of(j)) * p.e_sk;
+                if (p.e != nullptr) sv += load1<BF16>(p.e, eo);
+                if (p.et != nullptr) {
+#pragma unroll
+                  for (int t = 0; t < T; ++t) ds[t][jt][r] += load1<BF16>(p.et, t * p.et_stride + eo);
+                }
+              }
+              sv *= kLog2e;
+            } else {
+              sv *= s2scale;
+            }
+            sc[jt][r] = valid ? sv : -INFINITY;
+#pragma unroll
+            for (int t = 0; t < T; ++t) ds[t][jt][r] = valid ? ds[t][jt][r] : 0.f;
+            mx = fmaxf(mx, sc[jt][r]);
+          }
         }
       }
 
@@ -413,6 +441,15 @@ __global__ void __launch_bounds__(kThreads, 1) mhsea_fwd_bf16_large_kernel(const
     float mut[TT];
 #pragma unroll
     for (int t = 0; t < T; ++t) mut[t] = group_sum(mu[t]) * inv;
+    if constexpr (!HAS_E) {
+      // the tangent scale, deferred from the scores (see above)
+#pragma unroll
+      for (int t = 0; t < T; ++t) {
+        mut[t] *= stscale;
+#pragma unroll
+        for (int dt = 0; dt < DT; ++dt) at[t][dt] *= stscale;
+      }
+    }
     if (qvalid) {
       const int64_t obase = bnhd(b, qsite, h, N, H, D);
 #pragma unroll
