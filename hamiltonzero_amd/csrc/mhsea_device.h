@@ -148,15 +148,24 @@ __device__ __forceinline__ void store1<BF16>(void* base, int64_t off, float a) {
 }
 
 // Sum / max over the four lane groups g that share one column c (lanes c, c+16, c+32, c+48).
-__device__ __forceinline__ float group_sum(float x) {
-  x += __shfl_xor(x, 16, 64);
-  x += __shfl_xor(x, 32, 64);
-  return x;
+// v_permlane16_swap / v_permlane32_swap with both operands x hand each lane the pair
+// {x[l], x[l ^ 16]} (resp. x[l ^ 32]) in VALU registers, without a round trip through
+// the LDS crossbar; the pair is combined in an order-independent way, so every lane of a
+// column ends with the same bits as the xor-shuffle reduction.
+__device__ __forceinline__ float xor16_pair_sum(float x) {
+  const auto s = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return __uint_as_float(s[0]) + __uint_as_float(s[1]);
 }
+__device__ __forceinline__ float xor32_pair_sum(float x) {
+  const auto s = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return __uint_as_float(s[0]) + __uint_as_float(s[1]);
+}
+__device__ __forceinline__ float group_sum(float x) { return xor32_pair_sum(xor16_pair_sum(x)); }
 __device__ __forceinline__ float group_max(float x) {
-  x = fmaxf(x, __shfl_xor(x, 16, 64));
-  x = fmaxf(x, __shfl_xor(x, 32, 64));
-  return x;
+  auto s = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  x = fmaxf(__uint_as_float(s[0]), __uint_as_float(s[1]));
+  s = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return fmaxf(__uint_as_float(s[0]), __uint_as_float(s[1]));
 }
 
 // Offset of element (b, n, h, d) of a [B, N, H, D] tensor.

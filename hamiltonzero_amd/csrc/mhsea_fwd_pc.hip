@@ -312,24 +312,30 @@ struct QSet {
   int b, h, n_phys, qsite;  // qsite: site of this lane's query (any in-range site if invalid)
 };
 
+// DG consecutive floats at byte offset voff of buffer r (16- or 8-byte loads).
 template <int DG>
-__device__ __forceinline__ void load_frag_f32(const float* base, int64_t off, float* dst) {
+__device__ __forceinline__ void buf_frag(__amdgpu_buffer_rsrc_t r, int voff, float* dst) {
   if constexpr (DG >= 4) {
 #pragma unroll
     for (int s = 0; s < DG; s += 4) {
-      const float4 x = *reinterpret_cast<const float4*>(base + off + s);
-      dst[s] = x.x;
-      dst[s + 1] = x.y;
-      dst[s + 2] = x.z;
-      dst[s + 3] = x.w;
+      const u32x4_t x = __builtin_amdgcn_raw_buffer_load_b128(r, voff + 4 * s, 0, 0);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) dst[s + i] = __uint_as_float(x[i]);
     }
   } else {
-    const float2 x = *reinterpret_cast<const float2*>(base + off);
-    dst[0] = x.x;
-    dst[1] = x.y;
+#pragma unroll
+    for (int s = 0; s < DG; s += 2) {
+      const auto x = __builtin_amdgcn_raw_buffer_load_b64(r, voff + 4 * s, 0, 0);
+      dst[s] = __uint_as_float(x[0]);
+      dst[s + 1] = __uint_as_float(x[1]);
+    }
   }
 }
 
+// Query fragments of one 16-query tile of item (b, h): lane (g, c) takes floats
+// g*DG .. g*DG+DG-1 of query row c of the tile. Every address is a 32-bit offset into the
+// walker's slice of the tensor (b and h are uniform over the wave, so the descriptors are
+// scalar); a tangent-free call reads from an empty descriptor, which yields zeros.
 template <int D, int T, bool GIVEN_LSE>
 __device__ __forceinline__ void pc_load_q(const FwdParams& p, QSet<D, T>& qs, int b, int h, int n_phys,
                                           const int16_t* slot_perm, int tile) {
@@ -342,27 +348,33 @@ __device__ __forceinline__ void pc_load_q(const FwdParams& p, QSet<D, T>& qs, in
   const int nq = pc_nq(n_phys, km, N);
   const int s_raw = km ? jq : static_cast<int>(slot_perm[jq & 63]);
   const int site = (jq < nq) ? s_raw : 0;  // always an in-range row
+  // b and h are wave-uniform but may reach here through branches the compiler cannot
+  // prove uniform; readfirstlane keeps the descriptors below in scalar registers.
+  b = __builtin_amdgcn_readfirstlane(b);
+  h = __builtin_amdgcn_readfirstlane(h);
   qs.b = b;
   qs.h = h;
   qs.n_phys = n_phys;
   qs.qsite = site;
-  const int64_t qoff = bnhd(b, site, h, N, H, D) + g * Sh::DG;
-  const float* qt = static_cast<const float*>(p.qt != nullptr ? p.qt : p.q);
-  const int64_t qts = p.qt != nullptr ? p.t_stride : 0;
-  load_frag_f32<Sh::DG>(static_cast<const float*>(p.q), qoff, qs.qf);
+  const int64_t wrow = static_cast<int64_t>(N) * H * D;  // floats per walker
+  const int wbytes = static_cast<int>(wrow * 4);
+  const int row = (site * H + h) * D;
+  const int qoff = (row + g * Sh::DG) * 4;
+  buf_frag<Sh::DG>(make_rsrc(static_cast<const float*>(p.q) + b * wrow, wbytes), qoff, qs.qf);
 #pragma unroll
-  for (int t = 0; t < T; ++t) load_frag_f32<Sh::DG>(qt, t * qts + qoff, qs.qtf[t]);
+  for (int t = 0; t < T; ++t) {
+    const float* qt = p.qt != nullptr ? static_cast<const float*>(p.qt) + t * p.t_stride + b * wrow
+                                      : static_cast<const float*>(p.q);
+    buf_frag<Sh::DG>(make_rsrc(qt, p.qt != nullptr ? wbytes : 0), qoff, qs.qtf[t]);
+  }
   if constexpr (GIVEN_LSE) {
-    qs.lse_in = p.lse_in[(static_cast<int64_t>(b) * N + site) * H + h];
-    const int64_t obase = bnhd(b, site, h, N, H, D);
+    const __amdgpu_buffer_rsrc_t l_rs = make_rsrc(p.lse_in + static_cast<int64_t>(b) * N * H, N * H * 4);
+    qs.lse_in = buf_load1(l_rs, (site * H + h) * 4);
+    const __amdgpu_buffer_rsrc_t o_rs = make_rsrc(static_cast<const float*>(p.out_in) + b * wrow, wbytes);
 #pragma unroll
     for (int dt = 0; dt < Sh::DT; ++dt) {
       const int d0 = (D % 16 == 0) ? dt * 16 + 4 * g : min(dt * 16 + 4 * g, D - 4);
-      const float4 x = *reinterpret_cast<const float4*>(static_cast<const float*>(p.out_in) + obase + d0);
-      qs.oin[dt][0] = x.x;
-      qs.oin[dt][1] = x.y;
-      qs.oin[dt][2] = x.z;
-      qs.oin[dt][3] = x.w;
+      buf_frag<4>(o_rs, (row + d0) * 4, qs.oin[dt]);
     }
   }
 }
@@ -404,7 +416,7 @@ __device__ __forceinline__ void pc_tile(const FwdParams& p, const char* buf, con
   const int g = lane >> 4, c = lane & 15;
   const int N = p.N, H = p.H;
   const bool km = p.key_mask != 0;
-  const int b = qs.b, h = qs.h;
+  const int b = __builtin_amdgcn_readfirstlane(qs.b), h = __builtin_amdgcn_readfirstlane(qs.h);
   const int nk = pc_nk(qs.n_phys, km, N);
   const int nq = pc_nq(qs.n_phys, km, N);
   const bool key_all = km && qs.n_phys == 0;
@@ -441,7 +453,9 @@ __device__ __forceinline__ void pc_tile(const FwdParams& p, const char* buf, con
   }
   pf();
 
-  const float qscale = qvalid ? p.scale : 0.f;
+  // Scores are formed in base 2: log2(e) rides on the query scale, so S^T and dS^T leave
+  // the matrix cores already multiplied by it; the tangent epilogue takes ln(2) back.
+  const float qscale = qvalid ? p.scale * kLog2e : 0.f;
   const float qtscale = p.qt != nullptr ? qscale : 0.f;
   float qf[DG], qtf[TT][DG];
 #pragma unroll
@@ -545,21 +559,21 @@ __device__ __forceinline__ void pc_tile(const FwdParams& p, const char* buf, con
       }
   compiler_fence();
 
-  // ---- bias, validity, base-2 scores --------------------------------------------------
+  // ---- bias, validity (only the last key tile can hold padding), max ----------------
   float mx = -INFINITY;
 #pragma unroll
   for (int jt = 0; jt < NJ; ++jt) {
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
       const int j = jt * 16 + 4 * r + g;
-      const bool valid = j < nk;
+      const bool valid = jt < NJ - 1 || j < nk;
       float sv = sc[jt][r];
       if constexpr (HAS_E) {
-        sv += ev[jt][r];
+        sv = fmaf(ev[jt][r], kLog2e, sv);
 #pragma unroll
-        for (int t = 0; t < T; ++t) ds[t][jt][r] += etv[t][jt][r];
+        for (int t = 0; t < T; ++t) ds[t][jt][r] = fmaf(etv[t][jt][r], kLog2e, ds[t][jt][r]);
       }
-      sc[jt][r] = valid ? sv * kLog2e : -INFINITY;
+      sc[jt][r] = valid ? sv : -INFINITY;
 #pragma unroll
       for (int t = 0; t < T; ++t) ds[t][jt][r] = valid ? ds[t][jt][r] : 0.f;
       mx = fmaxf(mx, sc[jt][r]);
@@ -628,11 +642,13 @@ __device__ __forceinline__ void pc_tile(const FwdParams& p, const char* buf, con
   float inv = 1.f, ltot = 0.f;
   if constexpr (!GIVEN_LSE) {
     ltot = group_sum(lsum);
-    inv = 1.f / ltot;
+    inv = __builtin_amdgcn_rcpf(ltot);  // ltot >= 1: the maximum key contributes 2^0
   }
+  // A^T and mu carry the log2(e) of dS^T; ln(2) folds into their scale factors.
+  const float inv_ln2 = inv * kLn2;
   float mut[TT];
 #pragma unroll
-  for (int t = 0; t < T; ++t) mut[t] = group_sum(mu[t]) * inv;
+  for (int t = 0; t < T; ++t) mut[t] = group_sum(mu[t]) * inv_ln2;
 
   float ov[DT][4];
 #pragma unroll
@@ -668,7 +684,7 @@ __device__ __forceinline__ void pc_tile(const FwdParams& p, const char* buf, con
       const int voff = (qvalid && (D % 16 == 0 || d0 < D)) ? (obase + d0) * 4 : obytes;
       float tv[4];
 #pragma unroll
-      for (int r = 0; r < 4; ++r) tv[r] = (at[t][dt][r] + ct[t][dt][r]) * inv - mut[t] * ov[dt][r];
+      for (int r = 0; r < 4; ++r) tv[r] = fmaf(-mut[t], ov[dt][r], fmaf(at[t][dt][r], inv_ln2, ct[t][dt][r] * inv));
       buf_store4(t_rs, voff, tv[0], tv[1], tv[2], tv[3]);
     }
   }
@@ -717,10 +733,16 @@ __device__ __forceinline__ void pc_consumer(const FwdParams& p, const char* lds,
       sq();
     }
     // A fourth query tile (n > 48) goes to consumer 0, with its fragments loaded here.
+    // The tile count must be the item's own: padding is only masked in the last key tile.
     if (wave == 0 && 3 * 16 < nq) {
       QSet<D, T> q3;
       pc_load_q<D, T, GIVEN_LSE>(p, q3, qs.b, qs.h, qs.n_phys, sp, 3);
-      pc_tile<D, T, GIVEN_LSE, HAS_E, 4>(p, buf, sp, q3, 3, [] {}, [] {});
+      switch ((nk + 15) >> 4) {
+        case 1: pc_tile<D, T, GIVEN_LSE, HAS_E, 1>(p, buf, sp, q3, 3, [] {}, [] {}); break;
+        case 2: pc_tile<D, T, GIVEN_LSE, HAS_E, 2>(p, buf, sp, q3, 3, [] {}, [] {}); break;
+        case 3: pc_tile<D, T, GIVEN_LSE, HAS_E, 3>(p, buf, sp, q3, 3, [] {}, [] {}); break;
+        default: pc_tile<D, T, GIVEN_LSE, HAS_E, 4>(p, buf, sp, q3, 3, [] {}, [] {}); break;
+      }
     }
     __builtin_amdgcn_s_waitcnt(kWaitLgkm0);
   };

@@ -60,7 +60,8 @@ def make_inputs(seed, B, N, H, D, n_phys, *, scattered=False, with_e=False, e_la
     dout = rng.standard_normal(shape, dtype=np.float32)
     mask = np.zeros((B, N), dtype=bool)
     for b in range(B):
-        sites = rng.permutation(N)[:n_phys] if scattered else np.arange(n_phys)
+        n_b = int(rng.integers(0, N + 1)) if n_phys < 0 else n_phys  # n_phys < 0: per-walker counts
+        sites = rng.permutation(N)[:n_b] if scattered else np.arange(n_b)
         mask[b, sites] = True
     arrs = dict(q=q, k=k, v=v, e=e, qt=tan[0], kt=tan[1], vt=tan[2], et=et, dout=dout)
     if bf16:
@@ -97,6 +98,12 @@ CASES = [
     ("c5_small_bf16", 1, 1024, 2, 64, 1000, False, False, "qhk", False, 1.0, 2, True),
     ("keymask_all_masked", 3, 16, 2, 32, 0, False, True, "qkh", True, 1.0, 1, False),
     ("square_all_masked", 3, 16, 2, 32, 0, False, True, "qhk", False, 1.0, 1, False),
+    # 32 < N <= 64, float32: one, two, three and four query tiles per item, and walkers whose
+    # site counts differ from item to item
+    ("n48_one_qtile_bias", 5, 48, 3, 32, 10, True, True, "qhk", False, 1.0, 1, False),
+    ("n64_keymask_d16_t2", 4, 64, 2, 16, 40, True, False, "qhk", True, 1.0, 2, False),
+    ("n40_d8_t2_bias", 3, 40, 2, 8, 25, True, True, "qkh", False, 0.5, 2, False),
+    ("n64_mixed_counts", 24, 64, 3, 32, -1, True, True, "qhk", False, 1.0, 1, False),
 ]
 IDS = [c[0] for c in CASES]
 
