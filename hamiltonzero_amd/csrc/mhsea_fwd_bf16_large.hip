@@ -5,7 +5,8 @@
 // consecutive compacted queries; each wave owns 16 of them. Keys are streamed in chunks of
 // 64 compacted keys through a double-buffered LDS pipeline: while the waves multiply chunk
 // i from one buffer, chunk i+1 (loaded into registers during chunk i-1) is written to the
-// other buffer and chunk i+2's global reads are issued. One barrier per chunk. A chunk is
+// other buffer and chunk i+2's global reads are issued, both behind chunk i's first
+// products. One barrier per chunk. A chunk is
 // staged once per 128 queries (not per 64), halving the key traffic of the 4-wave kernel.
 //
 // LDS layout per buffer: K and Kt[t] row-major ([key][d], rows padded to D + 8 bf16),
@@ -284,13 +285,16 @@ __global__ void __launch_bounds__(kThreads, 1) mhsea_fwd_bf16_large_kernel(const
     const int kc = ch * kKC;
     const uint16_t* const Kb = lds + (ch & 1) * Sh::kBuf;
     const uint16_t* const Vb = Kb + NX * Sh::kRow;
-    // stage chunk ch+1 (in registers since chunk ch-1) into the other buffer, then start
-    // the reads of chunk ch+2
-    if (ch + 1 < nchunks) {
-      chunk_store((ch + 1) & 1);
-      if (ch + 2 < nchunks) chunk_load(kc + 2 * kKC);
-    }
-
+    // Stage chunk ch+1 (in registers since chunk ch-1) into the other buffer, then start
+    // the reads of chunk ch+2. A computing wave does it right after issuing this chunk's
+    // S^T and dS^T products, so the LDS writes and the read issue overlap the matrix cores.
+    auto stage = [&]() {
+      if (ch + 1 < nchunks) {
+        chunk_store((ch + 1) & 1);
+        if (ch + 2 < nchunks) chunk_load(kc + 2 * kKC);
+      }
+    };
+    if (!active) stage();
     if (active) {
       const int jn = min(kKC, nk - kc);
       const int njt = (jn + 15) >> 4;
@@ -316,6 +320,7 @@ __global__ void __launch_bounds__(kThreads, 1) mhsea_fwd_bf16_large_kernel(const
         }
       }
 
+      stage();
       // Base-2 scores. A full chunk (every key physical) needs no validity selects. Without
       // a bias the tangent scores stay unscaled here: P o dS is linear in the scale, which
       // is applied once to A and mu at the end.
