@@ -172,33 +172,52 @@ __global__ void __launch_bounds__(kThreads, 1) mhsea_fwd_bf16_large_kernel(const
   };
 
   // ---- chunk staging: global -> registers (load), registers -> LDS buffer (store) -----
+  // A thread's staging items sit at the same place of every chunk, so their tensor (one
+  // per wave: 64 divides the items of a tensor), descriptor, row and column are fixed for
+  // the whole workgroup; per chunk only the rows' site offsets are looked up.
+  const int wv = __builtin_amdgcn_readfirstlane(wave);
+  __amdgpu_buffer_rsrc_t krs[Sh::kKPer], vrs[Sh::kVPer];
+  int krow[Sh::kKPer], kcol[Sh::kKPer], vkey[Sh::kVPer], vcol[Sh::kVPer];
+#pragma unroll
+  for (int u = 0; u < Sh::kKPer; ++u) {
+    const int it = tid + u * kThreads;
+    const int x = (wv * 64 + u * kThreads) / (kKC * C8);  // wave-uniform
+    krs[u] = pick(kr, min(x, NX - 1));
+    const int rem = it % (kKC * C8);
+    krow[u] = rem / C8;
+    kcol[u] = (rem % C8) * 16;
+  }
+#pragma unroll
+  for (int u = 0; u < Sh::kVPer; ++u) {
+    const int it = tid + u * kThreads;
+    const int x = (wv * 64 + u * kThreads) / ((kKC / 4) * C8);  // wave-uniform
+    vrs[u] = pick(vr, min(x, NX - 1));
+    const int rem = it % ((kKC / 4) * C8);
+    vkey[u] = 4 * (rem % (kKC / 4));
+    vcol[u] = (rem / (kKC / 4)) * 16;
+  }
   uint4 rk[Sh::kKPer];
   uint4 rv[Sh::kVPer][4];
+  // Site-list reads are unconditional (clamped index) and all precede the loads, so they
+  // share one LDS wait.
+  auto row_off = [&](int j) {
+    const int sj = idx[min(j, N - 1)];
+    return j < nk ? (key_all ? j : sj) * rowstride + hoff : wbytes;
+  };
   auto chunk_load = [&](int kc) {
+    int koff[Sh::kKPer], voff[Sh::kVPer][4];
 #pragma unroll
-    for (int u = 0; u < Sh::kKPer; ++u) {
-      const int it = tid + u * kThreads;
-      const bool item_ok = Sh::kKItems % kThreads == 0 || it < Sh::kKItems;
-      // the tensor of an item is uniform across a wave (64 | kKC * C8): a scalar index
-      const int x = __builtin_amdgcn_readfirstlane(item_ok ? it / (kKC * C8) : 0);
-      const int rem = it % (kKC * C8);
-      const int off = key_off(kc + rem / C8);
-      rk[u] = bload(pick(kr, x), off == wbytes ? off : off + (rem % C8) * 16);
-    }
+    for (int u = 0; u < Sh::kKPer; ++u) koff[u] = row_off(kc + krow[u]);
 #pragma unroll
-    for (int u = 0; u < Sh::kVPer; ++u) {
-      const int it = tid + u * kThreads;
-      const bool unit_ok = Sh::kVUnits % kThreads == 0 || it < Sh::kVUnits;
-      // uniform across a wave (64 | (kKC / 4) * C8)
-      const int x = __builtin_amdgcn_readfirstlane(unit_ok ? it / ((kKC / 4) * C8) : 0);
-      const int rem = it % ((kKC / 4) * C8);
-      const int kg = rem % (kKC / 4), dg = rem / (kKC / 4);
+    for (int u = 0; u < Sh::kVPer; ++u)
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int off = key_off(kc + 4 * kg + i);
-        rv[u][i] = bload(pick(vr, x), off == wbytes ? off : off + dg * 16);
-      }
-    }
+      for (int i = 0; i < 4; ++i) voff[u][i] = row_off(kc + vkey[u] + i);
+#pragma unroll
+    for (int u = 0; u < Sh::kKPer; ++u) rk[u] = bload(krs[u], koff[u] == wbytes ? wbytes : koff[u] + kcol[u]);
+#pragma unroll
+    for (int u = 0; u < Sh::kVPer; ++u)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) rv[u][i] = bload(vrs[u], voff[u][i] == wbytes ? wbytes : voff[u][i] + vcol[u]);
   };
   auto chunk_store = [&](int buf) {
     uint16_t* const base = lds + buf * Sh::kBuf;
