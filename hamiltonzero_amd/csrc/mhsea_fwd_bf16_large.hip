@@ -305,15 +305,19 @@ __global__ void __launch_bounds__(kThreads, 1) mhsea_fwd_bf16_large_kernel(const
     const uint16_t* const Kb = lds + (ch & 1) * Sh::kBuf;
     const uint16_t* const Vb = Kb + NX * Sh::kRow;
     // Stage chunk ch+1 (in registers since chunk ch-1) into the other buffer, then start
-    // the reads of chunk ch+2. A computing wave does it right after issuing this chunk's
-    // S^T and dS^T products, so the LDS writes and the read issue overlap the matrix cores.
+    // the reads of chunk ch+2. A computing wave writes right after issuing this chunk's
+    // S^T and dS^T products and issues the reads right before its P.V products, so both
+    // overlap matrix-core work.
     auto stage = [&]() {
-      if (ch + 1 < nchunks) {
-        chunk_store((ch + 1) & 1);
-        if (ch + 2 < nchunks) chunk_load(kc + 2 * kKC);
-      }
+      if (ch + 1 < nchunks) chunk_store((ch + 1) & 1);
     };
-    if (!active) stage();
+    auto stage2 = [&]() {
+      if (ch + 2 < nchunks) chunk_load(kc + 2 * kKC);
+    };
+    if (!active) {
+      stage();
+      stage2();
+    }
     if (active) {
       const int jn = min(kKC, nk - kc);
       const int njt = (jn + 15) >> 4;
@@ -426,6 +430,7 @@ __global__ void __launch_bounds__(kThreads, 1) mhsea_fwd_bf16_large_kernel(const
           mu[t] += (ds[t][jt][0] + ds[t][jt][1]) + (ds[t][jt][2] + ds[t][jt][3]);
         }
 
+      stage2();
       // ---- P.V products over key pairs ------------------------------------------------
 #pragma unroll
       for (int pp = 0; pp < NJT / 2; ++pp) {
