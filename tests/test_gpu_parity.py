@@ -104,6 +104,14 @@ CASES = [
     ("n64_keymask_d16_t2", 4, 64, 2, 16, 40, True, False, "qhk", True, 1.0, 2, False),
     ("n40_d8_t2_bias", 3, 40, 2, 8, 25, True, True, "qkh", False, 0.5, 2, False),
     ("n64_mixed_counts", 24, 64, 3, 32, -1, True, True, "qhk", False, 1.0, 1, False),
+    # N > 128, bfloat16: the 64-key chunk pipeline with one, two, three and more chunks,
+    # a partial last chunk, bias in both layouts, the key mask (including no physical
+    # site, where every site is a key) and walkers whose site counts differ
+    ("n144_bf16_one_chunk", 3, 144, 1, 64, 40, True, False, "qhk", False, 1.0, 1, True),
+    ("n160_bf16_keymask_t2", 2, 160, 2, 64, 70, True, True, "qkh", True, 1.0, 2, True),
+    ("n200_bf16_d32_bias", 2, 200, 2, 32, 150, True, True, "qhk", False, 0.8, 1, True),
+    ("n136_bf16_keymask_none", 2, 136, 1, 32, 0, False, False, "qhk", True, 1.0, 1, True),
+    ("n256_bf16_mixed_t2", 6, 256, 2, 32, -1, True, True, "qhk", False, 1.0, 2, True),
 ]
 IDS = [c[0] for c in CASES]
 
