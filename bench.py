@@ -8,7 +8,7 @@ Prints ONE JSON line with walkers/s, the roofline of the dominant kernel (live H
 timing on the launch stream) and a CPU baseline (the jnp path's torch-CPU port, timed on
 a bounded walker sample on this host; see oracle/cpu_baseline.py).
 
-Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--config c1..c5]
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--config c1..c5|rect]
                        [--cpu-budget SECONDS] [--no-cpu-baseline]
 """
 
@@ -41,7 +41,104 @@ CONFIGS = {
            "large-N forward + JVP, fp32, [512,256,8,64], 225/256 physical sites (15x15)"),
     "c5": ("fwd_jvp", 128, 1024, 16, 64, 1000, 2, "bf16", 4,
            "large-N stress forward + 2 JVP directions, bf16 I/O, [128,1024,16,64], 1000/1024 sites"),
+    # The large-N evaluation forward (noncausal_bias_mha via pallas_rectangular_edge_attention):
+    # one system, all queries against all keys, dense [Nq, Nk, H] bias. Not a BASELINE.json
+    # configuration: reported beside the hot path, never as the default line.
+    "rect": ("rect", 1, 4096, 16, 64, 4000, 0, "f32", 5,
+             "rectangular forward with dense bias, fp32, one system, Nq=Nk=4096, H=16, D=64, "
+             "4000/4096 physical keys"),
 }
+RECT_METRIC = "rectangular large-N forward (noncausal_bias_mha) query rows/sec; % of MFMA/HBM roofline"
+
+
+def rect_algorithmic(B, Nq, Nk, H, D, n_phys):
+    """Bytes and flops of one rectangular forward. padded: q, k, v, out and the bias
+    [Nq, Nk, H] moved once, the key mask as uint8, 4 Nq Nk D flops per (system, head);
+    effective: only physical keys' k, v and bias columns, and their flops."""
+    row = H * D * 4
+    padded_bytes = B * (2 * Nq * row + 2 * Nk * row + Nq * Nk * H * 4 + Nk)
+    eff_bytes = B * (2 * Nq * row + 2 * n_phys * row + Nq * n_phys * H * 4 + Nk)
+    return dict(padded_bytes=padded_bytes, eff_bytes=eff_bytes,
+                padded_flops=B * H * 4 * Nq * Nk * D, eff_flops=B * H * 4 * Nq * n_phys * D)
+
+
+def run_rect(args, desc, B, N, H, D, n_phys, seed):
+    """Bench leg of the rectangular forward (hz_rect_attention_fwd)."""
+    import torch
+
+    from hamiltonzero_amd import _native
+
+    lib = _native.lib()
+    dev = torch.device("cuda:0")
+    rng = np.random.default_rng(seed)
+
+    def draw(shape, scale):
+        return torch.from_numpy(rng.standard_normal(shape, dtype=np.float32) * np.float32(scale)).to(dev)
+
+    q = draw((B, N, H, D), 1.0)
+    k = draw((B, N, H, D), 1.0)
+    v = draw((B, N, H, D), 1.0)
+    bias = draw((B, N, N, H), D ** -0.5)
+    mask = torch.zeros((B, N), dtype=torch.uint8, device=dev)
+    mask[:, :n_phys] = 1
+    out = torch.empty_like(q)
+    s = torch.cuda.current_stream(dev).cuda_stream
+    scale = D ** -0.5
+
+    def step():
+        _native.check(lib.hz_rect_attention_fwd(s, q.data_ptr(), k.data_ptr(), v.data_ptr(), bias.data_ptr(),
+                                                mask.data_ptr(), out.data_ptr(), B, N, N, H, D, scale))
+
+    ms = timed(step, args.steps, args.warmup, torch.cuda.current_stream(dev))
+    t_s = ms / 1e3
+    alg = rect_algorithmic(B, N, N, H, D, n_phys)
+    roof = roofline(alg["padded_bytes"], alg["padded_flops"], t_s, "f32")
+    roof["traffic"] = traffic_from_profile(args.config)
+    roof["basis"] = "padded algorithmic bytes/flops (every q, k, v, out row and the full bias once)"
+    roof["bytes_per_step"] = alg["padded_bytes"]
+    roof["flops_per_step"] = alg["padded_flops"]
+    roof_mask = roofline(alg["eff_bytes"], alg["eff_flops"], t_s, "f32")
+    roof_mask["basis"] = "mask-aware algorithmic bytes/flops (physical keys only)"
+    roof_mask["bytes_per_step"] = alg["eff_bytes"]
+    roof_mask["flops_per_step"] = alg["eff_flops"]
+    cpu = None
+    if not args.no_cpu_baseline:
+        from oracle import cpu_baseline
+
+        threads = int(os.environ.get("OMP_NUM_THREADS", os.cpu_count() or 1))
+        sample = 64
+        r = cpu_baseline.time_rect_queries_per_s(sample, N, H, D, n_phys, seed, budget_s=args.cpu_budget,
+                                                 threads=threads)
+        cpu = {"value": r["queries_per_s"], "unit": "queries/s", "cores": r["threads"], "kind": "port",
+               "sample": f"{sample} query rows of one system against all {N} keys, {r['reps']} reps in "
+                         f"{r['seconds']:.1f} s, torch-CPU fp32 port of the jnp formula ({r['cpu_model']})"}
+    line = {
+        "metric": RECT_METRIC, "value": B * N / t_s, "unit": "queries/s", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": ms, "higher_is_better": True, "scaling": "weak",
+        "vs_baseline": None, "dtype": "f32", "data": "synthetic (numpy default_rng, N(0,1) q/k/v, N(0,1)/sqrt(D) bias)",
+        "config": {"workload": f"rect: {desc}", "B": B, "Nq": N, "Nk": N, "H": H, "D": D, "n_phys": n_phys},
+        "roofline": roof, "roofline_mask_aware": roof_mask, "cpu_baseline": cpu,
+    }
+    print(json.dumps(line), flush=True)
+    return 0
+
+
+def timed(step, steps, warmup, stream):
+    """Average milliseconds of ``step`` over ``steps`` launches after ``warmup``, with HIP
+    events recorded on the launch stream."""
+    import torch
+
+    for _ in range(warmup):
+        step()
+    torch.cuda.synchronize()
+    ev0 = torch.cuda.Event(enable_timing=True)
+    ev1 = torch.cuda.Event(enable_timing=True)
+    ev0.record(stream)
+    for _ in range(steps):
+        step()
+    ev1.record(stream)
+    torch.cuda.synchronize()
+    return ev0.elapsed_time(ev1) / steps
 
 
 def algorithmic(work, B, N, H, D, n_phys, T, esize):
@@ -149,6 +246,8 @@ def main(argv=None):
 
     lib = _native.lib()
     work, B, N, H, D, n_phys, T, dtype, seed, desc = CONFIGS[args.config]
+    if work == "rect":
+        return run_rect(args, desc, B, N, H, D, n_phys, seed)
     tdt = torch.bfloat16 if dtype == "bf16" else torch.float32
     hz_dtype = _native.HZ_DTYPE_BF16 if dtype == "bf16" else _native.HZ_DTYPE_F32
     esize = 2 if dtype == "bf16" else 4
@@ -202,29 +301,24 @@ def main(argv=None):
             _native.check(lib.hz_mhsea_bwd(s, P(q), P(k), None, P(v), P(mask), P(lse), P(out), P(dout),
                                            P(dq), P(dk), None, P(dv), B, N, H, D, hz_dtype, 1.0, fl))
 
-    for _ in range(args.warmup):
-        step()
-    torch.cuda.synchronize()
-    ev0 = torch.cuda.Event(enable_timing=True)
-    ev1 = torch.cuda.Event(enable_timing=True)
-    ev0.record(stream)
-    for _ in range(args.steps):
-        step()
-    ev1.record(stream)
-    torch.cuda.synchronize()
-    ms = ev0.elapsed_time(ev1) / args.steps
+    ms = timed(step, args.steps, args.warmup, stream)
     t_s = ms / 1e3
     walkers_s = B / t_s
 
     alg = algorithmic(work, B, N, H, D, n_phys, T, esize)
-    roof = roofline(alg["eff_bytes"], alg["eff_flops"], t_s, dtype)
+    # roofline: the per-walker algorithmic bytes / flops of the padded problem (every
+    # [B,N,H,D] tensor moved once, (2+4T)G / 6G / 2G flops), the figure the reference's
+    # own kernels are sized by. roofline_mask_aware: the stricter figure that counts only
+    # physical input rows and physical x physical pairs (what this kernel must do).
+    roof = roofline(alg["padded_bytes"], alg["padded_flops"], t_s, dtype)
     roof["traffic"] = traffic_from_profile(args.config)
-    roof["basis"] = "mask-aware algorithmic bytes/flops (physical rows in, all rows out)"
-    roof["bytes_per_step"] = alg["eff_bytes"]
-    roof["flops_per_step"] = alg["eff_flops"]
-    roof_padded = roofline(alg["padded_bytes"], alg["padded_flops"], t_s, dtype)
-    roof_padded["bytes_per_step"] = alg["padded_bytes"]
-    roof_padded["flops_per_step"] = alg["padded_flops"]
+    roof["basis"] = "padded algorithmic bytes/flops per walker x B (every row of every tensor once)"
+    roof["bytes_per_step"] = alg["padded_bytes"]
+    roof["flops_per_step"] = alg["padded_flops"]
+    roof_mask = roofline(alg["eff_bytes"], alg["eff_flops"], t_s, dtype)
+    roof_mask["basis"] = "mask-aware algorithmic bytes/flops (physical rows in, all rows out)"
+    roof_mask["bytes_per_step"] = alg["eff_bytes"]
+    roof_mask["flops_per_step"] = alg["eff_flops"]
 
     cpu = None
     if not args.no_cpu_baseline:
@@ -261,7 +355,7 @@ def main(argv=None):
                    "n_phys": n_phys, "T": T, "work": work,
                    "kernels": "generic" if args.generic else "auto"},
         "roofline": roof,
-        "roofline_padded": roof_padded,
+        "roofline_mask_aware": roof_mask,
         "cpu_baseline": cpu,
     }
     print(json.dumps(line), flush=True)

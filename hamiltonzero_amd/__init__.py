@@ -6,8 +6,12 @@ Public surface, named after the reference modules it replaces:
   ``reference_edge_attention`` (``src/hamiltonzero/model/pallas_attention.py``).
 * :mod:`hamiltonzero_amd.mhsea_tuned` — ``mhsea_with_tuned_ad`` and the primitive pair
   (``src/hamiltonzero/model/_pallas_attn/mhsea_tuned.py``).
+* :mod:`hamiltonzero_amd.rect_attention` — ``noncausal_bias_mha`` and
+  ``pallas_rectangular_edge_attention`` (``src/hamiltonzero/evaluation/pallas_mha.py``,
+  ``src/hamiltonzero/evaluation/sequence_parallel.py``), the large-N evaluation forward.
 * :mod:`hamiltonzero_amd.kernels` — tensor-level calls of the C ABI
-  (``include/hz_mhsea.h``): forward, tangent, fused forward+tangent, backward.
+  (``include/hz_mhsea.h``): forward, tangent, fused forward+tangent, backward,
+  rectangular forward.
 """
 
 from .edge_attention import mhsea_tuned_edge_attention, reference_edge_attention
@@ -19,8 +23,10 @@ from .mhsea_tuned import (
     mhsea_tuned_jvp,
     mhsea_with_tuned_ad,
 )
+from .rect_attention import BlockSizes, noncausal_bias_mha, pallas_rectangular_edge_attention
 
 __all__ = [
+    "BlockSizes",
     "mhsea_ad",
     "mhsea_tuned_ad",
     "mhsea_tuned_ad_lin",
@@ -28,5 +34,7 @@ __all__ = [
     "mhsea_tuned_edge_attention",
     "mhsea_tuned_jvp",
     "mhsea_with_tuned_ad",
+    "noncausal_bias_mha",
+    "pallas_rectangular_edge_attention",
     "reference_edge_attention",
 ]

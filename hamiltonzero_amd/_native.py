@@ -33,6 +33,7 @@ EXPORTED_SYMBOLS = (
     "hz_mhsea_jvp",
     "hz_mhsea_fwd_jvp",
     "hz_mhsea_bwd",
+    "hz_rect_attention_fwd",
 )
 
 
@@ -76,6 +77,8 @@ _SIGNATURES = {
         [_P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _INT, _F, _INT],
         _INT,
     ),
+    # stream, q, k, v, bias, key_mask, out, B, Nq, Nk, H, D, scale
+    "hz_rect_attention_fwd": ([_P, _P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _F], _INT),
 }
 
 

@@ -92,4 +92,19 @@ hipError_t device_cu_count(int* cus);
 hipError_t launch_fwd_small(const FwdParams& p, int D, int T, bool given_lse, int dtype,
                             hipStream_t stream);
 
+// Rectangular attention with a dense [B, Nq, Nk, H] bias (rect_attention.hip).
+struct RectParams {
+  const float* q;      // [B, Nq, H, D]
+  const float* k;      // [B, Nk, H, D]
+  const float* v;      // [B, Nk, H, D]
+  const float* bias;   // [B, Nq, Nk, H]; may be null (zero bias)
+  const uint8_t* key_mask;  // [B, Nk]; may be null (every key physical)
+  float* out;          // [B, Nq, H, D]
+  int B, Nq, Nk, H;
+  float scale;
+};
+hipError_t launch_rect_fwd(const RectParams& p, int D, hipStream_t stream);
+// Dynamic LDS the rectangular kernel needs (largest variant for this D, H).
+size_t rect_fwd_lds_bytes(int D, int H, int Nk, bool masked);
+
 }  // namespace hz

@@ -258,3 +258,46 @@ def mhsea_bwd(
         )
     )
     return dq, dk, de, dv
+
+
+def rect_attention_fwd(
+    q: Tensor,
+    k: Tensor,
+    v: Tensor,
+    bias: Optional[Tensor] = None,
+    key_mask: Optional[Tensor] = None,
+    scale: float = 1.0,
+) -> Tensor:
+    """Rectangular attention with a dense pair bias (``hz_rect_attention_fwd``).
+
+    ``q [B, Nq, H, D]``, ``k, v [B, Nk, H, D]``, ``bias [B, Nq, Nk, H]`` (None: zero),
+    ``key_mask [B, Nk]`` (None: every key); float32. Returns ``out [B, Nq, H, D]`` of
+    ``softmax_j(scale q.k + where(key_mask, bias, -1e30)) v``.
+    """
+    if q.dim() != 4 or k.dim() != 4 or v.dim() != 4:
+        raise ValueError("q, k and v must have rank 4 [B, N, H, D]")
+    B, Nq, H, D = q.shape
+    Nk = k.shape[1]
+    for name, t in (("q", q), ("k", k), ("v", v), ("bias", bias)):
+        if t is not None and t.dtype != torch.float32:
+            raise TypeError(f"{name}.dtype must be float32, got {t.dtype}")
+    if not q.is_cuda:
+        raise ValueError("rectangular attention needs GPU tensors (q is on %s)" % q.device)
+    if D not in SUPPORTED_HEAD_DIMS:
+        raise ValueError(f"head dimension must be one of {list(SUPPORTED_HEAD_DIMS)}, got {D}")
+    if tuple(k.shape) != (B, Nk, H, D) or tuple(v.shape) != (B, Nk, H, D):
+        raise ValueError(f"k and v must have shape {(B, Nk, H, D)}, got {tuple(k.shape)} and {tuple(v.shape)}")
+    if bias is not None and tuple(bias.shape) != (B, Nq, Nk, H):
+        raise ValueError(f"bias must have shape {(B, Nq, Nk, H)}, got {tuple(bias.shape)}")
+    if key_mask is not None and tuple(key_mask.shape) != (B, Nk):
+        raise ValueError(f"key_mask must have shape {(B, Nk)}, got {tuple(key_mask.shape)}")
+    q, k, v, bias = map(_c, (q, k, v, bias))
+    m = None if key_mask is None else _mask_u8(key_mask, q.device)
+    out = torch.empty_like(q)
+    _native.check(
+        _native.lib().hz_rect_attention_fwd(
+            _stream(q.device), _ptr(q), _ptr(k), _ptr(v), _ptr(bias), _ptr(m), _ptr(out),
+            B, Nq, Nk, H, D, float(scale),
+        )
+    )
+    return out

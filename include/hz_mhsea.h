@@ -148,6 +148,28 @@ int hz_mhsea_bwd(hipStream_t stream,
                  int64_t B, int64_t N, int64_t H, int64_t D,
                  int dtype, float scale, int flags);
 
+/*
+ * Rectangular attention with a dense pair bias, forward only (the large-N evaluation
+ * path). Replaces noncausal_bias_mha (src/hamiltonzero/evaluation/pallas_mha.py:92-161,
+ * kernel :43-89) and its wrapper pallas_rectangular_edge_attention
+ * (src/hamiltonzero/evaluation/sequence_parallel.py:59-90):
+ *     out[b,i,h] = sum_j softmax_j(scale q[b,i,h].k[b,j,h] + bias'[b,i,j,h]) v[b,j,h]
+ *     bias'      = key_mask[b,j] ? bias[b,i,j,h] : -1e30      (sequence_parallel.py:79-83)
+ * Layouts: q, out [B, Nq, H, D]; k, v [B, Nk, H, D]; bias [B, Nq, Nk, H] (heads innermost,
+ * the reference's [batch, query, key, heads], pallas_mha.py:111); key_mask [B, Nk] uint8.
+ * Nq and Nk are independent (a sequence-parallel rank's local queries against all keys).
+ * float32 only, as the reference (sequence_parallel.py:42-47). noncausal_bias_mha is
+ * scale = 1 with key_mask = NULL; the wrapper is scale = D^-1/2 with its mask.
+ * Optional: bias (NULL = zero), key_mask (NULL = every key physical). If no key of a
+ * system is physical every score is -1e30 and out is the mean of all Nk value rows, as in
+ * the reference's float32 arithmetic. 1 <= Nq, Nk <= HZ_MAX_N; D in {8, 16, 32, 64}.
+ */
+int hz_rect_attention_fwd(hipStream_t stream,
+                          const float* q, const float* k, const float* v,
+                          const float* bias, const uint8_t* key_mask, float* out,
+                          int64_t B, int64_t Nq, int64_t Nk, int64_t H, int64_t D,
+                          float scale);
+
 #ifdef __cplusplus
 }
 #endif

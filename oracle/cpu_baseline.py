@@ -102,3 +102,46 @@ def time_walkers_per_s(work: str, B: int, N: int, H: int, D: int, n_phys: int, s
         "threads": threads,
         "cpu_model": host_cpu_model(),
     }
+
+
+def rect_attention(q, k, v, bias, key_mask, scale):
+    """noncausal_bias_mha(q * scale, k, v, where(key_mask, bias, -1e30)) in torch-CPU float32
+    (src/hamiltonzero/evaluation/sequence_parallel.py:79-90, pallas_mha.py:43-89)."""
+    e = torch.where(key_mask[:, None, :, None], bias, torch.full((), -1e30, dtype=bias.dtype))
+    s = torch.einsum("bihd,bjhd->bhij", q * scale, k) + e.permute(0, 3, 1, 2)
+    return torch.einsum("bhij,bjhd->bihd", torch.softmax(s, dim=-1), v)
+
+
+def time_rect_queries_per_s(Nq_sample: int, Nk: int, H: int, D: int, n_phys: int, seed: int,
+                            budget_s: float = 15.0, threads: int | None = None) -> dict:
+    """Time the rectangular forward for ``Nq_sample`` query rows of one system against all
+    ``Nk`` keys (a sequence-parallel rank's share); returns query rows per second."""
+    threads = threads or os.cpu_count() or 1
+    torch.set_num_threads(threads)
+    rng = np.random.default_rng(seed)
+
+    def draw(shape, scale):
+        return torch.from_numpy(rng.standard_normal(shape, dtype=np.float32) * np.float32(scale))
+
+    q = draw((1, Nq_sample, H, D), 1.0)
+    k = draw((1, Nk, H, D), 1.0)
+    v = draw((1, Nk, H, D), 1.0)
+    bias = draw((1, Nq_sample, Nk, H), D ** -0.5)
+    mask = torch.zeros((1, Nk), dtype=torch.bool)
+    mask[:, :n_phys] = True
+    with torch.no_grad():
+        rect_attention(q, k, v, bias, mask, D ** -0.5)  # warm-up
+        reps, t0 = 0, time.perf_counter()
+        while True:
+            rect_attention(q, k, v, bias, mask, D ** -0.5)
+            reps += 1
+            el = time.perf_counter() - t0
+            if el >= budget_s or reps >= 100000:
+                break
+    return {
+        "queries_per_s": Nq_sample * reps / el,
+        "seconds": el,
+        "reps": reps,
+        "threads": threads,
+        "cpu_model": host_cpu_model(),
+    }

@@ -119,3 +119,31 @@ def test_signatures_declared(lib):
     assert len(lib.hz_mhsea_jvp.argtypes) == 21
     assert len(lib.hz_mhsea_fwd_jvp.argtypes) == 21
     assert len(lib.hz_mhsea_bwd.argtypes) == 20
+
+
+def test_rect_rejects_bad_arguments(lib):
+    # stream, q, k, v, bias, key_mask, out, B, Nq, Nk, H, D, scale
+    base = [None, A, A, A, None, None, A, 1, 256, 1024, 16, 64, 0.125]
+
+    def call(**over):
+        args = list(base)
+        names = ["stream", "q", "k", "v", "bias", "key_mask", "out", "B", "Nq", "Nk", "H", "D", "scale"]
+        for key, val in over.items():
+            args[names.index(key)] = val
+        return lib.hz_rect_attention_fwd(*args)
+
+    cases = [
+        (dict(D=24), _native.HZ_EINVAL, "head dimension"),
+        (dict(Nq=0), _native.HZ_EINVAL, "positive"),
+        (dict(Nk=0), _native.HZ_EINVAL, "positive"),
+        (dict(Nk=_native.HZ_MAX_N + 1), _native.HZ_EINVAL, "Nk must be"),
+        (dict(H=0), _native.HZ_EINVAL, "B and H"),
+        (dict(q=None), _native.HZ_ENULL, "q must not be NULL"),
+        (dict(out=None), _native.HZ_ENULL, "out"),
+        (dict(bias=A + 4), _native.HZ_EALIGN, "bias"),
+        (dict(scale=float("inf")), _native.HZ_EINVAL, "scale"),
+    ]
+    for over, code, needle in cases:
+        assert call(**over) == code, over
+        assert needle in lib.hz_last_error().decode(), over
+    assert len(lib.hz_rect_attention_fwd.argtypes) == 13
