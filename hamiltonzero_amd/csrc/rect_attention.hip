@@ -111,6 +111,85 @@ __device__ __forceinline__ int compact_keys(const uint8_t* __restrict__ mask_row
   return total;
 }
 
+// What the staging steps of one workgroup need (fixed for the whole kernel).
+struct StageArgs {
+  const float* kbase;  // k of this system at head h0
+  const float* vbase;
+  const float* ebase;  // bias of this system at head h0; null = no bias
+  const int16_t* idx;  // physical keys (LDS), used when gather
+  int nk, Nq, Nk, H, q0;
+  bool gather;
+};
+
+// Issue the global loads of key chunk [kc, kc + KC) into registers: the K and V rows of
+// the workgroup's HG heads (one contiguous HG*D run per key) and the bias block
+// [QB queries][KC keys][HG heads]. Every load is in bounds (padding rows read key 0 /
+// the last query row); padding is zeroed or ignored when the chunk is written to LDS.
+template <int D, int HG, int QT, int KVP, int BP>
+__device__ __forceinline__ void rect_load_chunk(float4 (&rk)[KVP], float4 (&rv)[KVP], BiasVec<HG> (&re)[BP],
+                                                const StageArgs& a, int kc) {
+  using Sh = RectShape<D, HG, QT>;
+  const int tid = threadIdx.x;
+#pragma unroll
+  for (int u = 0; u < Sh::kKvPerThread; ++u) {
+    const int it = tid + u * Sh::NT;
+    const int j = kc + it / Sh::kRowItems;
+    const bool ok = (Sh::kKvItems % Sh::NT == 0 || it < Sh::kKvItems) && j < a.nk;
+    const int n = ok ? (a.gather ? a.idx[j] : j) : 0;
+    const int64_t off = static_cast<int64_t>(n) * a.H * D + (it % Sh::kRowItems) * 4;
+    rk[u] = *reinterpret_cast<const float4*>(a.kbase + off);
+    rv[u] = *reinterpret_cast<const float4*>(a.vbase + off);
+  }
+  if (a.ebase != nullptr) {
+#pragma unroll
+    for (int u = 0; u < Sh::kBiasPerThread; ++u) {
+      const int it = tid + u * Sh::NT;
+      const int qi = it / Sh::KC;
+      const int j = kc + it % Sh::KC;
+      const int qrow = a.q0 + qi < a.Nq ? a.q0 + qi : a.Nq - 1;
+      const int n = j < a.nk ? (a.gather ? a.idx[j] : j) : 0;
+      re[u].load(a.ebase + (static_cast<int64_t>(qrow) * a.Nk + n) * a.H);
+    }
+  }
+}
+
+// Write the staged chunk to LDS: K and V as [head][key][LD] (rows past the last key
+// zeroed), the bias as [head][query][KCP].
+template <int D, int HG, int QT, int KVP, int BP>
+__device__ __forceinline__ void rect_store_chunk(const float4 (&rk)[KVP], const float4 (&rv)[KVP],
+                                                 const BiasVec<HG> (&re)[BP], float* Ks, float* Vs, float* Es,
+                                                 const StageArgs& a, int kc) {
+  using Sh = RectShape<D, HG, QT>;
+  const int tid = threadIdx.x;
+#pragma unroll
+  for (int u = 0; u < Sh::kKvPerThread; ++u) {
+    const int it = tid + u * Sh::NT;
+    if (Sh::kKvItems % Sh::NT == 0 || it < Sh::kKvItems) {
+      const int r = it / Sh::kRowItems;
+      const int hh = (it % Sh::kRowItems) / Sh::C4;
+      const int c4 = it % Sh::C4;
+      const bool ok = kc + r < a.nk;
+      const int so = (hh * Sh::KC + r) * Sh::LD + c4 * 4;
+      // Component-wise selects: a select of whole float4 values is lowered through scratch.
+      const float4 x = rk[u], y = rv[u];
+      *reinterpret_cast<float4*>(Ks + so) =
+          make_float4(ok ? x.x : 0.f, ok ? x.y : 0.f, ok ? x.z : 0.f, ok ? x.w : 0.f);
+      *reinterpret_cast<float4*>(Vs + so) =
+          make_float4(ok ? y.x : 0.f, ok ? y.y : 0.f, ok ? y.z : 0.f, ok ? y.w : 0.f);
+    }
+  }
+  if (a.ebase != nullptr) {
+#pragma unroll
+    for (int u = 0; u < Sh::kBiasPerThread; ++u) {
+      const int it = tid + u * Sh::NT;
+      const int qi = it / Sh::KC;
+      const int j = it % Sh::KC;
+#pragma unroll
+      for (int hh = 0; hh < HG; ++hh) Es[(hh * Sh::QB + qi) * Sh::KCP + j] = re[u].get(hh);
+    }
+  }
+}
+
 template <int D, int HG, int QT>
 __global__ void __launch_bounds__(64 * QT * HG) rect_attention_fwd_kernel(const RectParams p) {
   using Sh = RectShape<D, HG, QT>;
@@ -166,60 +245,9 @@ __global__ void __launch_bounds__(64 * QT * HG) rect_attention_fwd_kernel(const 
   const float* const kbase = p.k + static_cast<int64_t>(b) * Nk * H * D + h0 * D;
   const float* const vbase = p.v + static_cast<int64_t>(b) * Nk * H * D + h0 * D;
   const float* const ebase = p.bias == nullptr ? nullptr : p.bias + static_cast<int64_t>(b) * Nq * Nk * H + h0;
+  const StageArgs sa{kbase, vbase, ebase, idx, nk, Nq, Nk, H, q0, gather};
 
-  auto load_chunk = [&](int kc) {
-#pragma unroll
-    for (int u = 0; u < KVP; ++u) {
-      const int it = tid + u * NT;
-      const int r = it / Sh::kRowItems;
-      const int j = kc + r;
-      const bool ok = (Sh::kKvItems % NT == 0 || it < Sh::kKvItems) && j < nk;
-      const int n = ok ? (gather ? idx[j] : j) : 0;
-      const int64_t off = static_cast<int64_t>(n) * H * D + (it % Sh::kRowItems) * 4;
-      rk[u] = *reinterpret_cast<const float4*>(kbase + off);
-      rv[u] = *reinterpret_cast<const float4*>(vbase + off);
-    }
-    if (ebase != nullptr) {
-#pragma unroll
-      for (int u = 0; u < BP; ++u) {
-        const int it = tid + u * NT;
-        const int qi = it / KC;
-        const int j = kc + it % KC;
-        const int qrow = q0 + qi < Nq ? q0 + qi : Nq - 1;
-        const int n = j < nk ? (gather ? idx[j] : j) : 0;
-        re[u].load(ebase + (static_cast<int64_t>(qrow) * Nk + n) * H);
-      }
-    }
-  };
-
-  auto store_chunk = [&](int kc) {
-#pragma unroll
-    for (int u = 0; u < KVP; ++u) {
-      const int it = tid + u * NT;
-      if (Sh::kKvItems % NT == 0 || it < Sh::kKvItems) {
-        const int r = it / Sh::kRowItems;
-        const int hh = (it % Sh::kRowItems) / C4;
-        const int c4 = it % C4;
-        const bool ok = kc + r < nk;
-        const int so = (hh * KC + r) * LD + c4 * 4;
-        const float4 z = make_float4(0.f, 0.f, 0.f, 0.f);
-        *reinterpret_cast<float4*>(Ks + so) = ok ? rk[u] : z;
-        *reinterpret_cast<float4*>(Vs + so) = ok ? rv[u] : z;
-      }
-    }
-    if (ebase != nullptr) {
-#pragma unroll
-      for (int u = 0; u < BP; ++u) {
-        const int it = tid + u * NT;
-        const int qi = it / KC;
-        const int j = it % KC;
-#pragma unroll
-        for (int hh = 0; hh < HG; ++hh) Es[(hh * QB + qi) * KCP + j] = re[u].get(hh);
-      }
-    }
-  };
-
-  load_chunk(0);
+  rect_load_chunk<D, HG, QT>(rk, rv, re, sa, 0);
 
   // Query fragment in B-operand layout: lane (g, c) holds q[q][h][g*DG .. g*DG + DG), scaled.
   const int qrow = q0 + qt * 16 + c;
@@ -261,18 +289,40 @@ __global__ void __launch_bounds__(64 * QT * HG) rect_attention_fwd_kernel(const 
 
   for (int kc = 0; kc < nk; kc += KC) {
     if (kc > 0) __syncthreads();  // every wave is done with the previous chunk
-    store_chunk(kc);
+    rect_store_chunk<D, HG, QT>(rk, rv, re, Ks, Vs, Es, sa, kc);
     __syncthreads();
-    if (kc + KC < nk) load_chunk(kc + KC);
+    if (kc + KC < nk) rect_load_chunk<D, HG, QT>(rk, rv, re, sa, kc + KC);
     if (!active) continue;
 
+    // Scores of the chunk's key tiles, the tiles' accumulator chains interleaved (one
+    // 16-byte K read per tile and four contraction steps).
     v4f sc[NJT];
 #pragma unroll
-    for (int jt = 0; jt < NJT; ++jt) {
-      sc[jt] = zero4();
-      const float* krow = Kw + (jt * 16 + c) * LD + g * DG;
+    for (int jt = 0; jt < NJT; ++jt) sc[jt] = zero4();
+    if constexpr (DG >= 4) {
 #pragma unroll
-      for (int s = 0; s < DG; ++s) sc[jt] = mfma16x4(krow[s], qf[s], sc[jt]);
+      for (int s = 0; s < DG; s += 4) {
+        float4 kv[NJT];
+#pragma unroll
+        for (int jt = 0; jt < NJT; ++jt)
+          kv[jt] = *reinterpret_cast<const float4*>(Kw + (jt * 16 + c) * LD + g * DG + s);
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int jt = 0; jt < NJT; ++jt) sc[jt] = mfma16x4(kv[jt].x, qf[s], sc[jt]);
+#pragma unroll
+        for (int jt = 0; jt < NJT; ++jt) sc[jt] = mfma16x4(kv[jt].y, qf[s + 1], sc[jt]);
+#pragma unroll
+        for (int jt = 0; jt < NJT; ++jt) sc[jt] = mfma16x4(kv[jt].z, qf[s + 2], sc[jt]);
+#pragma unroll
+        for (int jt = 0; jt < NJT; ++jt) sc[jt] = mfma16x4(kv[jt].w, qf[s + 3], sc[jt]);
+      }
+    } else {
+#pragma unroll
+      for (int jt = 0; jt < NJT; ++jt) {
+        const float* krow = Kw + (jt * 16 + c) * LD + g * DG;
+#pragma unroll
+        for (int s = 0; s < DG; ++s) sc[jt] = mfma16x4(krow[s], qf[s], sc[jt]);
+      }
     }
 
     float mx = -INFINITY;
@@ -303,18 +353,26 @@ __global__ void __launch_bounds__(64 * QT * HG) rect_attention_fwd_kernel(const 
       }
 
     // O^T += V^T P^T over the chunk's keys.
+    // Each key tile's V operands are read into registers before its products, so the
+    // LDS latency is paid once per tile rather than once per pair of products.
 #pragma unroll
-    for (int jt = 0; jt < NJT; ++jt)
+    for (int jt = 0; jt < NJT; ++jt) {
+      float va[4][DT];
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
         const float* vrow = Vw + (jt * 16 + 4 * g + r) * LD;
 #pragma unroll
         for (int dt = 0; dt < DT; ++dt) {
           const int col = dt * 16 + c;
-          const float va = (D % 16 == 0 || col < D) ? vrow[col] : 0.f;
-          o[dt] = mfma16x4(va, sc[jt][r], o[dt]);
+          va[r][dt] = (D % 16 == 0 || col < D) ? vrow[col] : 0.f;
         }
       }
+      __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+      for (int r = 0; r < 4; ++r)
+#pragma unroll
+        for (int dt = 0; dt < DT; ++dt) o[dt] = mfma16x4(va[r][dt], sc[jt][r], o[dt]);
+    }
   }
 
   if (active) {
