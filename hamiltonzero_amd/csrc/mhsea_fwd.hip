@@ -486,7 +486,7 @@ hipError_t launch_fwd(const FwdParams& p, int D, int T, bool given_lse, int dtyp
     if (dtype == 1 && bf16_fwd_supported(D)) return launch_fwd_bf16(p, D, T, given_lse, stream);
     if (small_fwd_supported(p.N, D, T)) return launch_fwd_small(p, D, T, given_lse, dtype, stream);
     if (pc_fwd_supported(p.N, p.H, D, T, dtype)) return launch_fwd_pc(p, D, T, given_lse, stream);
-    if (stream_fwd_supported(p.N)) return launch_fwd_stream(p, D, T, given_lse, dtype, stream);
+    if (stream_fwd_supported(p.N, D, T, dtype)) return launch_fwd_stream(p, D, T, given_lse, dtype, stream);
   }
   if (dtype == 1) return dispatch_d<BF16>(p, D, T, given_lse, stream);
   return dispatch_d<F32>(p, D, T, given_lse, stream);

@@ -330,12 +330,8 @@ hipError_t dispatch_nkt(const FwdParams& p, hipStream_t stream) {
   if constexpr (SmallFits<D, T>::kMaxKeyTiles >= 2) {
     if (nkt == 2) return launch_small_t<D, T, GIVEN_LSE, HAS_E, S, 2>(p, stream);
   }
-  if constexpr (SmallFits<D, T>::kMaxKeyTiles >= 3) {
-    if (nkt == 3) return launch_small_t<D, T, GIVEN_LSE, HAS_E, S, 3>(p, stream);
-  }
-  if constexpr (SmallFits<D, T>::kMaxKeyTiles >= 4) {
-    if (nkt == 4) return launch_small_t<D, T, GIVEN_LSE, HAS_E, S, 4>(p, stream);
-  }
+  // small_fwd_supported admits N <= 32, i.e. at most two key tiles; wider instantiations
+  // would be unreachable (and do not fit the register budget without spilling).
   return hipErrorInvalidValue;
 }
 

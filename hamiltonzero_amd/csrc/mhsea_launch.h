@@ -72,7 +72,7 @@ struct SmallFits {
   static constexpr int kMaxKeyTiles = small_max_key_tiles(D, T);
 };
 bool small_fwd_supported(int N, int D, int T);
-bool stream_fwd_supported(int N);
+bool stream_fwd_supported(int N, int D, int T, int dtype);
 hipError_t launch_fwd_stream(const FwdParams& p, int D, int T, bool given_lse, int dtype,
                              hipStream_t stream);
 bool stream_bwd_supported(int N);
