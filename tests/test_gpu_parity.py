@@ -104,6 +104,9 @@ CASES = [
     ("n64_keymask_d16_t2", 4, 64, 2, 16, 40, True, False, "qhk", True, 1.0, 2, False),
     ("n40_d8_t2_bias", 3, 40, 2, 8, 25, True, True, "qkh", False, 0.5, 2, False),
     ("n64_mixed_counts", 24, 64, 3, 32, -1, True, True, "qhk", False, 1.0, 1, False),
+    # float32 D = 64, N <= 64: one tangent (streaming kernel) and two (LDS-streaming kernel)
+    ("n64_d64_t1_fp32", 3, 64, 2, 64, 48, False, False, "qhk", False, 1.0, 1, False),
+    ("n64_d64_t2_fp32_bias", 3, 64, 2, 64, 48, True, True, "qkh", False, 0.5, 2, False),
     # N > 128, bfloat16: the 64-key chunk pipeline with one, two, three and more chunks,
     # a partial last chunk, bias in both layouts, the key mask (including no physical
     # site, where every site is a key) and walkers whose site counts differ
