@@ -66,6 +66,13 @@ struct Bf16Shape {
   static constexpr int kC8 = D / 8;           // 8-element (16 B) chunks of one row
   static constexpr int kItems = KC * kC8;     // 16 B items of one tensor chunk
   static constexpr int kPerThread = (kItems + 255) / 256;
+  // V staging at D = 64: one item = rows (2p, 2p+1) of one 8-column chunk, written transposed
+  // as 32-bit (row pair) words, so a wave's 32 pairs x 2 chunks cover 64 distinct LDS banks
+  // (one row per item and 16-bit writes put 8 lanes on each bank). At D = 32 the pairs would
+  // leave half of the threads without V items, so V is staged like K, one row per item.
+  static constexpr bool kPairV = D == 64;
+  static constexpr int kPairItems = (KC / 2) * kC8;
+  static constexpr int kPairPer = kPairV ? (kPairItems + 255) / 256 : 1;
   static size_t lds_bytes(int N) {
     const size_t n16 = (static_cast<size_t>(N) + 15) & ~size_t(15);
     return static_cast<size_t>((1 + T) * kRowTile + (1 + T) * kTrTile) * 2 + 16 + n16 + 2 * n16;
@@ -116,7 +123,10 @@ __global__ void __launch_bounds__(256, ((D == 64 && T > 0) ? 2 : 3)) mhsea_fwd_b
   const int64_t qts = has_qt ? p.t_stride : 0;
 
   // ---- key chunk staging: global (16 B of one row per item) -> registers -> LDS ---------
-  uint4 ck[NPT], cv[NPT], ckt[TT][NPT], cvt[TT][NPT];
+  constexpr int NPP = Sh::kPairPer;
+  uint4 ck[NPT], ckt[TT][NPT];
+  // V (and Vt): [pair item][row of the pair] at D = 64, [row item][0] otherwise
+  uint4 cv[Sh::kPairV ? NPP : NPT][2], cvt[TT][Sh::kPairV ? NPP : NPT][2];
   auto chunk_load = [&](int kc) {
 #pragma unroll
     for (int u = 0; u < NPT; ++u) {
@@ -125,14 +135,36 @@ __global__ void __launch_bounds__(256, ((D == 64 && T > 0) ? 2 : 3)) mhsea_fwd_b
       const bool ok = (Sh::kItems % 256 == 0 || it < Sh::kItems) && j < nk;
       const int n = ok ? (key_all ? j : idx[j]) : 0;
       const int64_t off = bnhd(b, n, h, N, H, D) + (it % C8) * 8;
-      const uint16_t* kb = static_cast<const uint16_t*>(p.k) + off;
-      ck[u] = *reinterpret_cast<const uint4*>(kb);
-      cv[u] = *reinterpret_cast<const uint4*>(static_cast<const uint16_t*>(p.v) + off);
+      ck[u] = *reinterpret_cast<const uint4*>(static_cast<const uint16_t*>(p.k) + off);
 #pragma unroll
-      for (int t = 0; t < T; ++t) {
+      for (int t = 0; t < T; ++t)
         ckt[t][u] = *reinterpret_cast<const uint4*>(static_cast<const uint16_t*>(ktp) + t * kts + off);
-        cvt[t][u] = *reinterpret_cast<const uint4*>(static_cast<const uint16_t*>(vtp) + t * vts + off);
+      if constexpr (!Sh::kPairV) {
+        cv[u][0] = *reinterpret_cast<const uint4*>(static_cast<const uint16_t*>(p.v) + off);
+#pragma unroll
+        for (int t = 0; t < T; ++t)
+          cvt[t][u][0] = *reinterpret_cast<const uint4*>(static_cast<const uint16_t*>(vtp) + t * vts + off);
       }
+    }
+    if constexpr (Sh::kPairV) {
+#pragma unroll
+    for (int u = 0; u < NPP; ++u) {
+      const int pi = tid + u * 256;
+      const bool live = Sh::kPairItems % 256 == 0 || pi < Sh::kPairItems;
+      const int pr = pi % 32;
+      const int kk = live ? pi / 32 : 0;  // 8-column chunk (in range also for idle threads)
+#pragma unroll
+      for (int h2 = 0; h2 < 2; ++h2) {
+        const int j = kc + 2 * pr + h2;
+        const bool ok = live && j < nk;
+        const int n = ok ? (key_all ? j : idx[j]) : 0;
+        const int64_t off = bnhd(b, n, h, N, H, D) + kk * 8;
+        cv[u][h2] = *reinterpret_cast<const uint4*>(static_cast<const uint16_t*>(p.v) + off);
+#pragma unroll
+        for (int t = 0; t < T; ++t)
+          cvt[t][u][h2] = *reinterpret_cast<const uint4*>(static_cast<const uint16_t*>(vtp) + t * vts + off);
+      }
+    }
     }
   };
   auto chunk_store = [&](int kc) {
@@ -144,17 +176,45 @@ __global__ void __launch_bounds__(256, ((D == 64 && T > 0) ? 2 : 3)) mhsea_fwd_b
         const int c8 = (it % C8) * 8;
         const bool ok = kc + r < nk;
         *reinterpret_cast<uint4*>(Kr + r * LDR + c8) = keep4(ok, ck[u]);
-        const uint4 vv = keep4(ok, cv[u]);
 #pragma unroll
-        for (int e = 0; e < 8; ++e) Vtr[(c8 + e) * LDT + r] = bf16_at(vv, e);
-#pragma unroll
-        for (int t = 0; t < T; ++t) {
+        for (int t = 0; t < T; ++t)
           *reinterpret_cast<uint4*>(Ktr + t * Sh::kRowTile + r * LDR + c8) = keep4(ok && has_kt, ckt[t][u]);
-          const uint4 tv = keep4(ok && has_vt, cvt[t][u]);
+        if constexpr (!Sh::kPairV) {
+          const uint4 vv = keep4(ok, cv[u][0]);
 #pragma unroll
-          for (int e = 0; e < 8; ++e) Vttr[t * Sh::kTrTile + (c8 + e) * LDT + r] = bf16_at(tv, e);
+          for (int e = 0; e < 8; ++e) Vtr[(c8 + e) * LDT + r] = bf16_at(vv, e);
+#pragma unroll
+          for (int t = 0; t < T; ++t) {
+            const uint4 tv = keep4(ok && has_vt, cvt[t][u][0]);
+#pragma unroll
+            for (int e = 0; e < 8; ++e) Vttr[t * Sh::kTrTile + (c8 + e) * LDT + r] = bf16_at(tv, e);
+          }
         }
       }
+    }
+    if constexpr (Sh::kPairV) {
+#pragma unroll
+    for (int u = 0; u < NPP; ++u) {
+      const int pi = tid + u * 256;
+      if (Sh::kPairItems % 256 == 0 || pi < Sh::kPairItems) {
+        const int r0 = 2 * (pi % 32);
+        const int c8 = (pi / 32) * 8;
+        const bool ok0 = kc + r0 < nk, ok1 = kc + r0 + 1 < nk;
+        const uint4 v0 = keep4(ok0, cv[u][0]), v1 = keep4(ok1, cv[u][1]);
+#pragma unroll
+        for (int e = 0; e < 8; ++e)
+          *reinterpret_cast<uint32_t*>(Vtr + (c8 + e) * LDT + r0) =
+              bf16_at(v0, e) | (static_cast<uint32_t>(bf16_at(v1, e)) << 16);
+#pragma unroll
+        for (int t = 0; t < T; ++t) {
+          const uint4 t0 = keep4(ok0 && has_vt, cvt[t][u][0]), t1 = keep4(ok1 && has_vt, cvt[t][u][1]);
+#pragma unroll
+          for (int e = 0; e < 8; ++e)
+            *reinterpret_cast<uint32_t*>(Vttr + t * Sh::kTrTile + (c8 + e) * LDT + r0) =
+                bf16_at(t0, e) | (static_cast<uint32_t>(bf16_at(t1, e)) << 16);
+        }
+      }
+    }
     }
   };
 
