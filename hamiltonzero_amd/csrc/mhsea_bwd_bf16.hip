@@ -50,9 +50,12 @@ template <int D>
 struct BwdBf16Shape {
   static constexpr int KC = 64;
   static constexpr int LDR = D + 8;   // row-major row, bf16 elements
-  // transposed row, bf16 elements: 66 makes the pairwise 32-bit transposed writes of one
-  // wave hit 64 distinct banks (row starts are then only 4-byte aligned)
-  static constexpr int LDT = KC + 2;
+  // transposed row, bf16 elements (35 words, row starts 4-byte aligned): the pairwise 32-bit
+  // transposed writes of one wave hit 64 distinct banks at D = 64 (two lanes per bank at
+  // D = 32), and the 32-bit operand reads (lane (g, c) at word 35c + 2g) put at most two
+  // lanes on a bank, the least any row stride allows for that read pattern (66 elements,
+  // 33 words, put four)
+  static constexpr int LDT = KC + 6;
   static constexpr int NS = D / 32;
   static constexpr int DT = D / 16;
   static constexpr int C8 = D / 8;
