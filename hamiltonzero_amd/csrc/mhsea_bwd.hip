@@ -397,7 +397,7 @@ hipError_t dispatch_d(const BwdParams& p, int D, hipStream_t stream) {
 
 hipError_t launch_bwd(const BwdParams& p, int D, int dtype, hipStream_t stream) {
   if (!p.force_generic) {
-    if (dtype == 1 && bf16_bwd_supported(p.N, D)) return launch_bwd_bf16(p, D, stream);
+    if (dtype == 1 && bf16_bwd_supported(p.N, p.H, D)) return launch_bwd_bf16(p, D, stream);
     if (stream_bwd_supported(p.N)) return launch_bwd_stream(p, D, dtype, stream);
   }
   if (dtype == 1) return dispatch_d<BF16>(p, D, stream);

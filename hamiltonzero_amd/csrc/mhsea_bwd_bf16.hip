@@ -66,6 +66,13 @@ struct BwdBf16Shape {
   static constexpr size_t kLdsBytes = static_cast<size_t>(4 * kRow + 3 * kTr) * 2 + 2 * KC * 4;
 };
 
+// Row `site` of one (walker, head) slice of a [B, N, H, D] tensor, relative to the slice's
+// first row: site * H * D elements. A full-rate 24-bit multiply: bf16_bwd_supported
+// guarantees H * D < 2^23 and site < 64, so the product needs no 64-bit arithmetic.
+__device__ __forceinline__ uint32_t row_off(int site, uint32_t hd) {
+  return __umul24(static_cast<uint32_t>(site), hd);
+}
+
 struct Sites {
   uint64_t bal;
   int perm;
@@ -104,6 +111,7 @@ __global__ void __launch_bounds__(256, 2) mhsea_bwd_bf16_kernel(const BwdParams 
   float* const Dls = L2s + Sh::KC;
 
   const int N = p.N, H = p.H;
+  const uint32_t HD = static_cast<uint32_t>(H * D);
   const int64_t nitems = static_cast<int64_t>(p.B) * H;
   const int64_t stride = gridDim.x;
   int64_t item = blockIdx.x;
@@ -131,22 +139,29 @@ __global__ void __launch_bounds__(256, 2) mhsea_bwd_bf16_kernel(const BwdParams 
   const int st_r0 = 2 * (tid / C8);
   auto issue_item_loads = [&](int b, int h, const Sites& st) {
     const int qperm = qperm_of(st), kperm = kperm_of(st), nq = nq_of(st), nk = nk_of(st);
+    // (walker, head) slice bases are wave-uniform; rows are 32-bit offsets from them
+    const int64_t base = bnhd(b, 0, h, N, H, D);
+    const uint16_t* const qw = static_cast<const uint16_t*>(p.q) + base;
+    const uint16_t* const gw = static_cast<const uint16_t*>(p.dout) + base;
+    const uint16_t* const ow = static_cast<const uint16_t*>(p.out) + base;
+    const uint16_t* const kw = static_cast<const uint16_t*>(p.k) + base;
+    const uint16_t* const vw = static_cast<const uint16_t*>(p.v) + base;
 #pragma unroll
     for (int u = 0; u < NPT; ++u) {
       if (!st_active) break;
       const int r = st_r0 + u;
       const int sq = __shfl(qperm, r & 63, 64);
       const int sk = __shfl(kperm, r & 63, 64);
-      const int64_t qoff = bnhd(b, r < nq ? sq : 0, h, N, H, D) + st_c8;
-      const int64_t koff = bnhd(b, r < nk ? sk : 0, h, N, H, D) + st_c8;
-      cq[u] = *reinterpret_cast<const uint4*>(static_cast<const uint16_t*>(p.q) + qoff);
-      cg[u] = *reinterpret_cast<const uint4*>(static_cast<const uint16_t*>(p.dout) + qoff);
-      co[u] = *reinterpret_cast<const uint4*>(static_cast<const uint16_t*>(p.out) + qoff);
-      ck[u] = *reinterpret_cast<const uint4*>(static_cast<const uint16_t*>(p.k) + koff);
-      cv[u] = *reinterpret_cast<const uint4*>(static_cast<const uint16_t*>(p.v) + koff);
+      const uint32_t qoff = row_off(r < nq ? sq : 0, HD) + st_c8;
+      const uint32_t koff = row_off(r < nk ? sk : 0, HD) + st_c8;
+      cq[u] = *reinterpret_cast<const uint4*>(qw + qoff);
+      cg[u] = *reinterpret_cast<const uint4*>(gw + qoff);
+      co[u] = *reinterpret_cast<const uint4*>(ow + qoff);
+      ck[u] = *reinterpret_cast<const uint4*>(kw + koff);
+      cv[u] = *reinterpret_cast<const uint4*>(vw + koff);
     }
     const int sl = __shfl(qperm, lane, 64);
-    clse = p.lse[(static_cast<int64_t>(b) * N + (lane < nq ? sl : 0)) * H + h];
+    clse = (p.lse + static_cast<int64_t>(b) * N * H + h)[__umul24(static_cast<uint32_t>(lane < nq ? sl : 0), static_cast<uint32_t>(H))];
   };
   auto load_mask_byte = [&](int b) -> uint32_t {
     return lane < N ? static_cast<uint32_t>(p.mask[static_cast<int64_t>(b) * N + lane]) : 0u;
@@ -215,6 +230,7 @@ __global__ void __launch_bounds__(256, 2) mhsea_bwd_bf16_kernel(const BwdParams 
     const int qperm = qperm_of(sc_), kperm = kperm_of(sc_);
     const int nqt = (nq + 15) >> 4, nkt = (nk + 15) >> 4;
     const int64_t e_walker = static_cast<int64_t>(bc) * N * N * H + static_cast<int64_t>(hc) * p.e_sh;
+    const int64_t obase_bh = bnhd(bc, 0, hc, N, H, D);  // wave-uniform slice base of the outputs
     const float scale = p.scale;
 
     // ---- phase A: dq (and de), wave = 16 queries ------------------------------------------
@@ -276,10 +292,11 @@ __global__ void __launch_bounds__(256, 2) mhsea_bwd_bf16_kernel(const BwdParams 
         }
       }
       if (qvalid) {
-        const int64_t obase = bnhd(bc, qsite, hc, N, H, D);
+        void* const dqw = static_cast<uint16_t*>(p.dq) + obase_bh;
+        const uint32_t orow = row_off(qsite, HD);
 #pragma unroll
         for (int dt = 0; dt < DT; ++dt)
-          store4<BF16>(p.dq, obase + dt * 16 + 4 * g, dqa[dt][0] * scale, dqa[dt][1] * scale,
+          store4<BF16>(dqw, orow + dt * 16 + 4 * g, dqa[dt][0] * scale, dqa[dt][1] * scale,
                        dqa[dt][2] * scale, dqa[dt][3] * scale);
       }
     }
@@ -340,12 +357,14 @@ __global__ void __launch_bounds__(256, 2) mhsea_bwd_bf16_kernel(const BwdParams 
         }
       }
       if (kvalid) {
-        const int64_t obase = bnhd(bc, ksite, hc, N, H, D);
+        void* const dkw = static_cast<uint16_t*>(p.dk) + obase_bh;
+        void* const dvw = static_cast<uint16_t*>(p.dv) + obase_bh;
+        const uint32_t orow = row_off(ksite, HD);
 #pragma unroll
         for (int dt = 0; dt < DT; ++dt) {
-          store4<BF16>(p.dk, obase + dt * 16 + 4 * g, dka[dt][0] * scale, dka[dt][1] * scale,
+          store4<BF16>(dkw, orow + dt * 16 + 4 * g, dka[dt][0] * scale, dka[dt][1] * scale,
                        dka[dt][2] * scale, dka[dt][3] * scale);
-          store4<BF16>(p.dv, obase + dt * 16 + 4 * g, dva[dt][0], dva[dt][1], dva[dt][2], dva[dt][3]);
+          store4<BF16>(dvw, orow + dt * 16 + 4 * g, dva[dt][0], dva[dt][1], dva[dt][2], dva[dt][3]);
         }
       }
     }
@@ -360,10 +379,10 @@ __global__ void __launch_bounds__(256, 2) mhsea_bwd_bf16_kernel(const BwdParams 
           const int it = base + tid;
           const int site = __shfl(sc_.perm, (sc_.n_phys + it / C4) & 63, 64);
           if (it < nmask * C4) {
-            const int64_t off = bnhd(bc, site, hc, N, H, D) + (it % C4) * 4;
-            if (!km) store4<BF16>(p.dq, off, 0.f, 0.f, 0.f, 0.f);
-            store4<BF16>(p.dk, off, 0.f, 0.f, 0.f, 0.f);
-            store4<BF16>(p.dv, off, 0.f, 0.f, 0.f, 0.f);
+            const uint32_t off = row_off(site, HD) + (it % C4) * 4;
+            if (!km) store4<BF16>(static_cast<uint16_t*>(p.dq) + obase_bh, off, 0.f, 0.f, 0.f, 0.f);
+            store4<BF16>(static_cast<uint16_t*>(p.dk) + obase_bh, off, 0.f, 0.f, 0.f, 0.f);
+            store4<BF16>(static_cast<uint16_t*>(p.dv) + obase_bh, off, 0.f, 0.f, 0.f, 0.f);
           }
         }
       }
@@ -412,7 +431,10 @@ hipError_t launch_t(const BwdParams& p, hipStream_t stream) {
 
 }  // namespace
 
-bool bf16_bwd_supported(int N, int D) { return N <= 64 && (D == 32 || D == 64); }
+bool bf16_bwd_supported(int N, int H, int D) {
+  // row offsets inside a (walker, head) slice use 24-bit multiplies (row_off)
+  return N <= 64 && (D == 32 || D == 64) && static_cast<int64_t>(H) * D < (int64_t(1) << 23);
+}
 
 hipError_t launch_bwd_bf16(const BwdParams& p, int D, hipStream_t stream) {
   const bool e = p.e != nullptr;

@@ -81,7 +81,7 @@ bool bf16_fwd_supported(int D);
 // Large-N bfloat16 kernel (N > 128): 128-query workgroups, double-buffered LDS key chunks.
 bool bf16_large_fwd_supported(int N, int D);
 hipError_t launch_fwd_bf16_large(const FwdParams& p, int D, int T, bool given_lse, hipStream_t stream);
-bool bf16_bwd_supported(int N, int D);
+bool bf16_bwd_supported(int N, int H, int D);
 hipError_t launch_bwd_bf16(const BwdParams& p, int D, hipStream_t stream);
 hipError_t launch_fwd_bf16(const FwdParams& p, int D, int T, bool given_lse, hipStream_t stream);
 // Producer/consumer kernel (float32, N <= 64): key tiles gathered into LDS.
