@@ -324,23 +324,31 @@ __global__ void __launch_bounds__(256, (D == 64 && T > 0) ? 2 : 3) mhsea_fwd_ker
       }
 
     // ---- O^T += V^T P^T ;  A^T += V^T (P o dS)^T ;  C^T += Vt^T P^T ------------------
+    // Per 4-key step, every V (and Vt) operand of the step is read before its products, so
+    // the LDS latency is paid once per step rather than once per product pair.
 #pragma unroll
     for (int jt = 0; jt < NJT; ++jt) {
       if (jt < njt) {
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
           const int row = jt * 16 + 4 * g + r;
+          float va[DT], vta[TT][DT];
 #pragma unroll
           for (int dt = 0; dt < DT; ++dt) {
             const int col = dt * 16 + c;
-            const float va = (D % 16 == 0 || col < D) ? Vs[row * LD + col] : 0.f;
-            if constexpr (!GIVEN_LSE) o[dt] = mfma16x4(va, sc[jt][r], o[dt]);
+            va[dt] = (D % 16 == 0 || col < D) ? Vs[row * LD + col] : 0.f;
+#pragma unroll
+            for (int t = 0; t < T; ++t)
+              vta[t][dt] = (D % 16 == 0 || col < D) ? Vts[t * Sh::kTileFloats + row * LD + col] : 0.f;
+          }
+          __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+          for (int dt = 0; dt < DT; ++dt) {
+            if constexpr (!GIVEN_LSE) o[dt] = mfma16x4(va[dt], sc[jt][r], o[dt]);
 #pragma unroll
             for (int t = 0; t < T; ++t) {
-              at[t][dt] = mfma16x4(va, ds[t][jt][r], at[t][dt]);
-              const float vta =
-                  (D % 16 == 0 || col < D) ? Vts[t * Sh::kTileFloats + row * LD + col] : 0.f;
-              ct[t][dt] = mfma16x4(vta, sc[jt][r], ct[t][dt]);
+              at[t][dt] = mfma16x4(va[dt], ds[t][jt][r], at[t][dt]);
+              ct[t][dt] = mfma16x4(vta[t][dt], sc[jt][r], ct[t][dt]);
             }
           }
         }
