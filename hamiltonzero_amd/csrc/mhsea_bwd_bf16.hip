@@ -10,6 +10,8 @@
 // d-contractions, 8 elements per lane) and transposed q, k, dout (A operands of the site
 // contractions: lane (g, c) of output row d reads sites kappa(g, i) = 16(2p + i/4) + 4g + i%4
 // as two 8-byte runs), plus lse*log2(e) and delta = rowsum(out o dout) in fp32.
+#include <atomic>
+
 #include "mhsea_device.h"
 #include "mhsea_launch.h"
 
@@ -412,12 +414,16 @@ hipError_t launch_t(const BwdParams& p, hipStream_t stream) {
                                          static_cast<int>(lds));
     if (err != hipSuccess) return err;
   }
-  static int per_cu = 0;
+  // occupancy of this instantiation, computed once; relaxed atomics keep concurrent
+  // first calls from several host threads free of data races
+  static std::atomic<int> per_cu_cache{0};
+  int per_cu = per_cu_cache.load(std::memory_order_relaxed);
   if (per_cu == 0) {
     int n = 0;
     hipError_t err = hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, reinterpret_cast<const void*>(kern), 256, lds);
     if (err != hipSuccess) return err;
     per_cu = n > 0 ? n : 1;
+    per_cu_cache.store(per_cu, std::memory_order_relaxed);
   }
   int cus = 0;
   hipError_t err = device_cu_count(&cus);

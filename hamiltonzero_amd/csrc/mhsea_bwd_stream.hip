@@ -13,6 +13,8 @@
 //  Phase B (key-major, wave = 16 keys): S = Q K^T and dP = dout V^T again (cheaper than a
 //    transpose of P and dS through LDS at this size), dv^T += dout^T P, dk^T += Q^T dS.
 // Every result row is written by exactly one wave: deterministic, no atomics.
+#include <atomic>
+
 #include "mhsea_device.h"
 #include "mhsea_launch.h"
 
@@ -360,12 +362,16 @@ hipError_t launch_bwd_stream_t(const BwdParams& p, hipStream_t stream) {
                                          static_cast<int>(lds));
     if (err != hipSuccess) return err;
   }
-  static int per_cu = 0;
+  // occupancy of this instantiation, computed once; relaxed atomics keep concurrent
+  // first calls from several host threads free of data races
+  static std::atomic<int> per_cu_cache{0};
+  int per_cu = per_cu_cache.load(std::memory_order_relaxed);
   if (per_cu == 0) {
     int n = 0;
     hipError_t err = hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, reinterpret_cast<const void*>(kern), 256, lds);
     if (err != hipSuccess) return err;
     per_cu = n > 0 ? n : 1;
+    per_cu_cache.store(per_cu, std::memory_order_relaxed);
   }
   int cus = 0;
   hipError_t err = device_cu_count(&cus);

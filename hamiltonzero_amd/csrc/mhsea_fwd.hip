@@ -21,6 +21,8 @@
 //   tout_i = sum_j P_ij dS_ij v_j + sum_j P_ij vt_j - (sum_j P_ij dS_ij) out_i   (:76-89)
 // The three sums are accumulated with the same online rescaling as out_i, so one pass
 // over the keys produces the primal and all T tangents.
+#include <atomic>
+
 #include "mhsea_device.h"
 #include "mhsea_launch.h"
 
@@ -470,19 +472,24 @@ hipError_t dispatch_d(const FwdParams& p, int D, int T, bool given_lse, hipStrea
 }  // namespace
 
 hipError_t device_cu_count(int* cus) {
+  // per-device cache; relaxed atomics keep concurrent calls from several host threads free
+  // of data races (every writer stores the same value)
   constexpr int kMaxDevices = 64;
-  static int cached[kMaxDevices] = {0};
+  static std::atomic<int> cached[kMaxDevices] = {};
   int dev = 0;
   hipError_t err = hipGetDevice(&dev);
   if (err != hipSuccess) return err;
-  if (dev >= 0 && dev < kMaxDevices && cached[dev] > 0) {
-    *cus = cached[dev];
-    return hipSuccess;
+  if (dev >= 0 && dev < kMaxDevices) {
+    const int c = cached[dev].load(std::memory_order_relaxed);
+    if (c > 0) {
+      *cus = c;
+      return hipSuccess;
+    }
   }
   int n = 0;
   err = hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev);
   if (err != hipSuccess) return err;
-  if (dev >= 0 && dev < kMaxDevices) cached[dev] = n;
+  if (dev >= 0 && dev < kMaxDevices) cached[dev].store(n, std::memory_order_relaxed);
   *cus = n;
   return hipSuccess;
 }

@@ -29,6 +29,8 @@
 // swizzled by (r / rows_per_128B) mod chunks_per_row, which keeps the consumers' K reads
 // (16 rows x one chunk) and V reads (4 rows x 16 floats) free of LDS bank conflicts at
 // D >= 32.
+#include <atomic>
+
 #include "mhsea_device.h"
 #include "mhsea_launch.h"
 
@@ -791,12 +793,16 @@ hipError_t launch_pc_t(const FwdParams& p, hipStream_t stream) {
                                          hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(lds));
     if (err != hipSuccess) return err;
   }
-  static int per_cu = 0;
+  // occupancy of this instantiation, computed once; relaxed atomics keep concurrent
+  // first calls from several host threads free of data races
+  static std::atomic<int> per_cu_cache{0};
+  int per_cu = per_cu_cache.load(std::memory_order_relaxed);
   if (per_cu == 0) {
     int n = 0;
     hipError_t err = hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, reinterpret_cast<const void*>(kern), 256, lds);
     if (err != hipSuccess) return err;
     per_cu = n > 0 ? n : 1;
+    per_cu_cache.store(per_cu, std::memory_order_relaxed);
   }
   int cus = 0;
   hipError_t err = device_cu_count(&cus);

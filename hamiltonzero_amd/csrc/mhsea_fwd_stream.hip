@@ -14,6 +14,8 @@
 // Per item the four waves each own a 16-query tile of the compacted list and use the
 // transposed orientation S^T = K Q^T, O^T += V^T P^T of the LDS-streaming kernel; the
 // softmax is exact (all keys in one chunk: max, exp, sum, no rescaling).
+#include <atomic>
+
 #include "mhsea_device.h"
 #include "mhsea_launch.h"
 
@@ -437,12 +439,16 @@ hipError_t launch_stream_t(const FwdParams& p, hipStream_t stream) {
   }
   // Enough workgroups to fill every CU at the occupancy the kernel's resources allow
   // (queried once per kernel; the CU count once per device).
-  static int per_cu = 0;
+  // occupancy of this instantiation, computed once; relaxed atomics keep concurrent
+  // first calls from several host threads free of data races
+  static std::atomic<int> per_cu_cache{0};
+  int per_cu = per_cu_cache.load(std::memory_order_relaxed);
   if (per_cu == 0) {
     int n = 0;
     hipError_t err = hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, reinterpret_cast<const void*>(kern), 256, lds);
     if (err != hipSuccess) return err;
     per_cu = n > 0 ? n : 1;
+    per_cu_cache.store(per_cu, std::memory_order_relaxed);
   }
   int cus = 0;
   hipError_t err = device_cu_count(&cus);
