@@ -1,4 +1,4 @@
-"""Throughput of the gfx950 MHSEA kernels on BASELINE.json's synthetic configurations.
+"""Throughput of the gfx950 MHSEA kernels on the path's synthetic benchmark configurations c1-c5.
 
 Default (the driver's run): configuration c2 — fused forward + JVP, float32,
 q/k/v [B=1024, N=64, H=8, D=32], one tangent per input, 36 physical sites of 64, seed 1.
@@ -42,8 +42,8 @@ CONFIGS = {
     "c5": ("fwd_jvp", 128, 1024, 16, 64, 1000, 2, "bf16", 4,
            "large-N stress forward + 2 JVP directions, bf16 I/O, [128,1024,16,64], 1000/1024 sites"),
     # The large-N evaluation forward (noncausal_bias_mha via pallas_rectangular_edge_attention):
-    # one system, all queries against all keys, dense [Nq, Nk, H] bias. Not a BASELINE.json
-    # configuration: reported beside the hot path, never as the default line.
+    # one system, all queries against all keys, dense [Nq, Nk, H] bias. Not one of c1-c5:
+    # reported beside the hot path, never as the default line.
     "rect": ("rect", 1, 4096, 16, 64, 4000, 0, "f32", 5,
              "rectangular forward with dense bias, fp32, one system, Nq=Nk=4096, H=16, D=64, "
              "4000/4096 physical keys"),
