@@ -2,14 +2,19 @@
 //
 // Same algebra and work decomposition as the fp32 persistent backward (custom_gradients.py:
 // 249-285, :307-347): per (walker, head) item, phase A (query-major) forms S^T, dP^T, P, dS
-// and dq^T = K^T dS^T (and de); phase B (key-major) forms S, dP again and dv^T = dout^T P,
-// dk^T = Q^T dS. Products run on v_mfma_f32_16x16x32_bf16 with fp32 accumulation; P, dS are
-// rounded to bf16 only as operands of the site contractions.
+// and dq^T = K^T dS^T (and de), and leaves P, dS in LDS as bf16; after a barrier phase B
+// (key-major) reads them back as B operands of dv^T = dout^T P, dk^T = Q^T dS. Products run on
+// v_mfma_f32_16x16x32_bf16 with fp32 accumulation; P, dS are rounded to bf16 only as operands
+// of the site contractions.
 //
 // LDS holds the compacted rows as bf16: row-major q, k, v, dout (A operands of the
 // d-contractions, 8 elements per lane) and transposed q, k, dout (A operands of the site
 // contractions: lane (g, c) of output row d reads sites kappa(g, i) = 16(2p + i/4) + 4g + i%4
-// as two 8-byte runs), plus lse*log2(e) and delta = rowsum(out o dout) in fp32.
+// as two 8-byte runs), plus lse*log2(e) and delta = rowsum(out o dout) in fp32, and P, dS as
+// four 16-query tiles of [key][query] rows (phase B's lane (g, c) reads key row c, queries
+// kappa(g, i), the same two-run pattern). At D = 64 the tile of query tile w overlays the q
+// (P) and dout (dS) rows of those 16 queries, which only wave w reads in phase A, before it
+// writes the tile.
 #include <atomic>
 
 #include "mhsea_device.h"
@@ -33,6 +38,10 @@ __device__ __forceinline__ uint16_t bf16_at(const uint4& u, int e) {
 }
 __device__ __forceinline__ float bf_lo(uint32_t w) { return __uint_as_float(w << 16); }
 __device__ __forceinline__ float bf_hi(uint32_t w) { return __uint_as_float(w & 0xffff0000u); }
+// The value of lane l ^ 1 (DPP quad permutation [1, 0, 3, 2]; every lane active).
+__device__ __forceinline__ float swap_lane_pair(float x) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), 0xB1, 0xF, 0xF, false));
+}
 __device__ __forceinline__ bf16x8 pack8(v4f a, v4f b) {
   uint4 u;
   u.x = pack2_bf16(a[0], a[1]);
@@ -65,7 +74,13 @@ struct BwdBf16Shape {
   static constexpr int kTr = D * LDT;
   // staging: one thread per (row pair, 8-column chunk); D = 32 leaves waves 2, 3 idle there
   static constexpr int kStageThreads = KC * C8 / 2;
-  static constexpr size_t kLdsBytes = static_cast<size_t>(4 * kRow + 3 * kTr) * 2 + 2 * KC * 4;
+  // P / dS tiles: 16 queries of one key per row, 2 elements of padding (9-word rows)
+  static constexpr int kPS = 18;
+  static constexpr int kPTile = KC * kPS;
+  // D = 64: 16 row-major rows of q (dout) are exactly one P (dS) tile
+  static constexpr bool kPAlias = 16 * LDR == kPTile;
+  static constexpr size_t kLdsBytes = static_cast<size_t>(4 * kRow + 3 * kTr) * 2 + 2 * KC * 4 +
+                                      (kPAlias ? 0 : static_cast<size_t>(2 * 4 * kPTile) * 2);
 };
 
 // Row `site` of one (walker, head) slice of a [B, N, H, D] tensor, relative to the slice's
@@ -111,6 +126,9 @@ __global__ void __launch_bounds__(256, 2) mhsea_bwd_bf16_kernel(const BwdParams 
   uint16_t* const GT = KT + Sh::kTr;
   float* const L2s = reinterpret_cast<float*>(GT + Sh::kTr);
   float* const Dls = L2s + Sh::KC;
+  uint16_t* const Pt = Sh::kPAlias ? Qr : reinterpret_cast<uint16_t*>(Dls + Sh::KC);
+  uint16_t* const DSt = Sh::kPAlias ? Gr : Pt + 4 * Sh::kPTile;
+  constexpr int kPS = Sh::kPS, kPTile = Sh::kPTile;
 
   const int N = p.N, H = p.H;
   const uint32_t HD = static_cast<uint32_t>(H * D);
@@ -250,6 +268,9 @@ __global__ void __launch_bounds__(256, 2) mhsea_bwd_bf16_kernel(const BwdParams 
       const float lse2 = L2s[jq];
       const float delta = Dls[jq];
       const int64_t e_row = e_walker + static_cast<int64_t>(qsite < 0 ? 0 : qsite) * p.e_sq;
+      const bool odd = (c & 1) != 0;
+      uint16_t* const ptile = Pt + wave * kPTile + (c & ~1);
+      uint16_t* const dstile = DSt + wave * kPTile + (c & ~1);
       v4f dsv[NT];
 #pragma unroll
       for (int jt = 0; jt < NT; ++jt) {
@@ -261,6 +282,7 @@ __global__ void __launch_bounds__(256, 2) mhsea_bwd_bf16_kernel(const BwdParams 
             sc = mfma_bf16(as_bf16x8(*reinterpret_cast<const uint4*>(Kr + (jt * 16 + c) * LDR + 32 * s + 8 * g)), qf[s], sc);
             dp = mfma_bf16(as_bf16x8(*reinterpret_cast<const uint4*>(Vr + (jt * 16 + c) * LDR + 32 * s + 8 * g)), gf[s], dp);
           }
+          float pv[4];
 #pragma unroll
           for (int r = 0; r < 4; ++r) {
             const int j = jt * 16 + 4 * g + r;
@@ -271,12 +293,24 @@ __global__ void __launch_bounds__(256, 2) mhsea_bwd_bf16_kernel(const BwdParams 
               ks = __shfl(kperm, j & 63, 64);
               if (valid) sv += load1<BF16>(p.e, e_row + static_cast<int64_t>(ks) * p.e_sk);
             }
-            const float pv = valid ? fast_exp2(sv * kLog2e - lse2) : 0.f;
-            dsv[jt][r] = pv * (dp[r] - delta);
+            pv[r] = valid ? fast_exp2(sv * kLog2e - lse2) : 0.f;
+            dsv[jt][r] = pv[r] * (dp[r] - delta);
             if (p.de != nullptr) {
               if constexpr (!HAS_E) ks = __shfl(kperm, j & 63, 64);
               if (valid) store1<BF16>(p.de, e_row + static_cast<int64_t>(ks) * p.e_sk, dsv[jt][r]);
             }
+          }
+          // P, dS of keys jt*16 + 4g + r into query tile `wave`: lanes c and c^1 trade one
+          // value per key pair, then each writes the (query c&~1, query c|1) word of one key
+          // (the even lane key r0, the odd lane key r0 + 1); invalid pairs hold zeros.
+#pragma unroll
+          for (int r0 = 0; r0 < 4; r0 += 2) {
+            const int row = (jt * 16 + 4 * g + r0 + (odd ? 1 : 0)) * kPS;
+            const float po = swap_lane_pair(odd ? pv[r0] : pv[r0 + 1]);
+            const float dso = swap_lane_pair(odd ? dsv[jt][r0] : dsv[jt][r0 + 1]);
+            *reinterpret_cast<uint32_t*>(ptile + row) = odd ? pack2_bf16(po, pv[r0 + 1]) : pack2_bf16(pv[r0], po);
+            *reinterpret_cast<uint32_t*>(dstile + row) =
+                odd ? pack2_bf16(dso, dsv[jt][r0 + 1]) : pack2_bf16(dsv[jt][r0], dso);
           }
         }
         __builtin_amdgcn_sched_barrier(0);
@@ -303,54 +337,34 @@ __global__ void __launch_bounds__(256, 2) mhsea_bwd_bf16_kernel(const BwdParams 
       }
     }
 
+    __syncthreads();  // the P, dS tiles of every query tile are written
+
     // ---- phase B: dk and dv, wave = 16 keys ---------------------------------------------
     if (wave < nkt) {
       const int jk = wave * 16 + c;
       const bool kvalid = jk < nk;
       const int ks_ = __shfl(kperm, jk & 63, 64);
       const int ksite = kvalid ? ks_ : -1;
-      bf16x8 kf[NS], vf[NS];
-#pragma unroll
-      for (int s = 0; s < NS; ++s) {
-        kf[s] = as_bf16x8(*reinterpret_cast<const uint4*>(Kr + jk * LDR + 32 * s + 8 * g));
-        vf[s] = as_bf16x8(*reinterpret_cast<const uint4*>(Vr + jk * LDR + 32 * s + 8 * g));
-      }
-      v4f pv[NT], dsv[NT];
-#pragma unroll
-      for (int it = 0; it < NT; ++it) {
-        pv[it] = dsv[it] = zero4();
-        if (it < nqt) {
-          v4f sc = zero4(), dp = zero4();
-#pragma unroll
-          for (int s = 0; s < NS; ++s) {
-            sc = mfma_bf16(as_bf16x8(*reinterpret_cast<const uint4*>(Qr + (it * 16 + c) * LDR + 32 * s + 8 * g)), kf[s], sc);
-            dp = mfma_bf16(as_bf16x8(*reinterpret_cast<const uint4*>(Gr + (it * 16 + c) * LDR + 32 * s + 8 * g)), vf[s], dp);
-          }
-#pragma unroll
-          for (int r = 0; r < 4; ++r) {
-            const int il = it * 16 + 4 * g + r;
-            const bool valid = il < nq && kvalid;
-            float sv = sc[r] * scale;
-            if constexpr (HAS_E) {
-              const int qs2 = __shfl(qperm, il & 63, 64);
-              if (valid)
-                sv += load1<BF16>(p.e, e_walker + static_cast<int64_t>(qs2) * p.e_sq +
-                                           static_cast<int64_t>(ksite) * p.e_sk);
-            }
-            pv[it][r] = valid ? fast_exp2(sv * kLog2e - L2s[il]) : 0.f;
-            dsv[it][r] = pv[it][r] * (dp[r] - Dls[il]);
-          }
+      // B operand of key jk over queries kappa(g, i) of query tiles 2pp, 2pp + 1 (the second
+      // is zero when phase A did not write it)
+      auto tile_operand = [&](const uint16_t* tiles, int pp) {
+        const uint32_t* w0 = reinterpret_cast<const uint32_t*>(tiles + 2 * pp * kPTile + jk * kPS + 4 * g);
+        uint4 u = make_uint4(w0[0], w0[1], 0u, 0u);
+        if (2 * pp + 1 < nqt) {
+          const uint32_t* w1 = w0 + kPTile / 2;
+          u.z = w1[0];
+          u.w = w1[1];
         }
-        __builtin_amdgcn_sched_barrier(0);
-      }
+        return as_bf16x8(u);
+      };
       v4f dka[DT], dva[DT];
 #pragma unroll
       for (int dt = 0; dt < DT; ++dt) dka[dt] = dva[dt] = zero4();
 #pragma unroll
       for (int pp = 0; pp < NT / 2; ++pp) {
         if (2 * pp < nqt) {
-          const bf16x8 pw = pack8(pv[2 * pp], pv[2 * pp + 1]);
-          const bf16x8 dw = pack8(dsv[2 * pp], dsv[2 * pp + 1]);
+          const bf16x8 pw = tile_operand(Pt, pp);
+          const bf16x8 dw = tile_operand(DSt, pp);
 #pragma unroll
           for (int dt = 0; dt < DT; ++dt) {
             dva[dt] = mfma_bf16(tr_operand(GT + (dt * 16 + c) * LDT + 32 * pp + 4 * g), pw, dva[dt]);

@@ -194,7 +194,7 @@ template <int D, int HG, int QT>
 __global__ void __launch_bounds__(64 * QT * HG) rect_attention_fwd_kernel(const RectParams p) {
   using Sh = RectShape<D, HG, QT>;
   constexpr int KC = Sh::KC, NJT = Sh::NJT, LD = Sh::LD, KCP = Sh::KCP, QB = Sh::QB;
-  constexpr int NT = Sh::NT, DG = Sh::DG, DT = Sh::DT, C4 = Sh::C4;
+  constexpr int DG = Sh::DG, DT = Sh::DT;
   constexpr int KVP = Sh::kKvPerThread, BP = Sh::kBiasPerThread;
 
   extern __shared__ float4 smem4[];
