@@ -32,6 +32,7 @@ EXPORTED_SYMBOLS = (
     "hz_mhsea_fwd",
     "hz_mhsea_jvp",
     "hz_mhsea_fwd_jvp",
+    "hz_mhsea_fwd_jvp_gated",
     "hz_mhsea_bwd",
     "hz_rect_attention_fwd",
 )
@@ -70,6 +71,11 @@ _SIGNATURES = {
     # stream, q, k, e, v, mask, qt, kt, et, vt, T, out, lse, tout, B, N, H, D, dtype, scale, flags
     "hz_mhsea_fwd_jvp": (
         [_P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _I64, _P, _P, _P, _I64, _I64, _I64, _I64, _INT, _F, _INT],
+        _INT,
+    ),
+    # stream, q, k, e, v, mask, qt, kt, et, vt, T, y, ty, B, N, H, D, scale, flags
+    "hz_mhsea_fwd_jvp_gated": (
+        [_P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _I64, _P, _P, _I64, _I64, _I64, _I64, _F, _INT],
         _INT,
     ),
     # stream, q, k, e, v, mask, lse, out, dout, dq, dk, de, dv, B, N, H, D, dtype, scale, flags

@@ -210,6 +210,58 @@ int hz_mhsea_fwd_jvp(hipStream_t stream, const void* q, const void* k, const voi
   return run_tangent_groups(p, D, T, false, dtype, stream, tout, qt, kt, et, vt);
 }
 
+int hz_mhsea_fwd_jvp_gated(hipStream_t stream, const void* q, const void* k, const void* e,
+                           const void* v, const uint8_t* mask, const void* qt, const void* kt,
+                           const void* et, const void* vt, int64_t T, void* y, void* ty,
+                           int64_t B, int64_t N, int64_t H, int64_t D, float scale, int flags) {
+  if (int rc = check_dims(B, N, H, D, HZ_DTYPE_F32, flags)) return rc;
+  if (T < 0 || T > 2) return fail(HZ_EINVAL, "T must be in [0, 2] for the gated collapse, got %lld", (long long)T);
+  if (H % 2 != 0) return fail(HZ_EINVAL, "the gated collapse pairs head h with h + H/2: H must be even, got %lld", (long long)H);
+  if (flags & HZ_FLAG_GENERIC) return fail(HZ_EINVAL, "HZ_FLAG_GENERIC is not available for the gated collapse");
+  // directions per pass: two where the kernel has the T = 2 variant (D <= 16), else one
+  auto served = [&](int t) {
+    return hz::pc_fwd_supported(static_cast<int>(N), static_cast<int>(H), static_cast<int>(D), t, HZ_DTYPE_F32);
+  };
+  if (!served(T < 1 ? 0 : 1))
+    return fail(HZ_EINVAL, "the gated collapse serves fp32, N <= 64, D in {8, 16, 32}; got N=%lld D=%lld", (long long)N,
+                (long long)D);
+  const int64_t tpass = served(2) ? 2 : 1;
+  HZ_REQUIRE(q);
+  HZ_REQUIRE(k);
+  HZ_REQUIRE(v);
+  if (mask == nullptr) return fail(HZ_ENULL, "mask must not be NULL");
+  HZ_REQUIRE(y);
+  if (T > 0) HZ_REQUIRE(ty);
+  HZ_OPTIONAL(e);
+  HZ_OPTIONAL(qt);
+  HZ_OPTIONAL(kt);
+  HZ_OPTIONAL(et);
+  HZ_OPTIONAL(vt);
+  if (!std::isfinite(scale)) return fail(HZ_EINVAL, "scale must be finite");
+  hz::FwdParams p = fwd_params(q, k, e, v, mask, B, N, H, D, scale, flags);
+  p.out = y;
+  p.lse = nullptr;
+  p.gated = 1;
+  p.y_tstride = B * N * (H / 2) * D;
+  if (T == 0) return launched(hz::launch_fwd_pc(p, static_cast<int>(D), 0, false, stream));
+  // Later passes rewrite identical y values, so the call needs no scratch memory.
+  const int64_t ts = p.t_stride, es = p.et_stride;
+  auto shift = [](const void* base, int64_t off) -> const void* {
+    return base == nullptr ? nullptr : static_cast<const float*>(base) + off;
+  };
+  for (int64_t t0 = 0; t0 < T; t0 += tpass) {
+    const int64_t tn = T - t0 < tpass ? T - t0 : tpass;
+    p.qt = shift(qt, t0 * ts);
+    p.kt = shift(kt, t0 * ts);
+    p.vt = shift(vt, t0 * ts);
+    p.et = shift(et, t0 * es);
+    p.tout = static_cast<float*>(ty) + t0 * p.y_tstride;
+    hipError_t err = hz::launch_fwd_pc(p, static_cast<int>(D), static_cast<int>(tn), false, stream);
+    if (err != hipSuccess) return launched(err);
+  }
+  return ok();
+}
+
 int hz_mhsea_bwd(hipStream_t stream, const void* q, const void* k, const void* e,
                  const void* v, const uint8_t* mask, const float* lse, const void* out,
                  const void* dout, void* dq, void* dk, void* de, void* dv, int64_t B,

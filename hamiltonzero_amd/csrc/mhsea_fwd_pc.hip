@@ -30,6 +30,7 @@
 // (16 rows x one chunk) and V reads (4 rows x 16 floats) free of LDS bank conflicts at
 // D >= 32.
 #include <atomic>
+#include <type_traits>
 
 #include "mhsea_device.h"
 #include "mhsea_launch.h"
@@ -96,6 +97,11 @@ __device__ __forceinline__ float buf_load1(__amdgpu_buffer_rsrc_t r, int voff) {
   return __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(r, voff, 0, 0));
 }
 
+__device__ __forceinline__ float4 buf_load4(__amdgpu_buffer_rsrc_t r, int voff) {
+  const u32x4_t v = __builtin_amdgcn_raw_buffer_load_b128(r, voff, 0, 0);
+  return make_float4(__uint_as_float(v.x), __uint_as_float(v.y), __uint_as_float(v.z), __uint_as_float(v.w));
+}
+
 __device__ __forceinline__ void compiler_fence() { asm volatile("" ::: "memory"); }
 
 // s_waitcnt immediates (gfx9 encoding: vmcnt[3:0]+[15:14], expcnt[6:4], lgkmcnt[11:8]).
@@ -133,10 +139,20 @@ __device__ __forceinline__ PcSites pc_sites(uint32_t mbyte, int N) {
 __device__ __forceinline__ int pc_nk(int n_phys, bool km, int N) { return (km && n_phys == 0) ? N : n_phys; }
 __device__ __forceinline__ int pc_nq(int n_phys, bool km, int N) { return km ? N : n_phys; }
 
+// Items of one workgroup: units first, first + stride, ...; a unit is a (walker, head), or
+// under the gated head collapse (half = H/2 > 0) a (walker, head pair) taken as two
+// consecutive items, the gate head hp (even k) and then the value head hp + H/2 (odd k).
 struct ItemSeq {
-  uint32_t first, stride, nitems, H;
+  uint32_t first, stride, nitems, H, half;
   __device__ __forceinline__ uint32_t item(int k) const { return first + static_cast<uint32_t>(k) * stride; }
   __device__ __forceinline__ void bh(int k, int& b, int& h) const {
+    if (half != 0) {
+      const uint32_t u = item(k >> 1);
+      const uint32_t bq = u / half;
+      b = static_cast<int>(bq);
+      h = static_cast<int>(u - bq * half) + (k & 1) * static_cast<int>(half);
+      return;
+    }
     const uint32_t it = item(k);
     const uint32_t bq = it / H;
     b = static_cast<int>(bq);
@@ -147,7 +163,7 @@ struct ItemSeq {
 // ------------------------------------------------------------------------------------
 // Producer (wave 3)
 // ------------------------------------------------------------------------------------
-template <int D, int T, bool GIVEN_LSE>
+template <int D, int T, bool GIVEN_LSE, bool GATED>
 __device__ __forceinline__ void pc_producer(const FwdParams& p, char* lds, const ItemSeq& seq, int cnt) {
   using Sh = PcShape<D, T>;
   const int lane = threadIdx.x & 63;
@@ -246,6 +262,14 @@ __device__ __forceinline__ void pc_producer(const FwdParams& p, char* lds, const
     for (int u = 0; u < NMI; ++u) {
       const int it = u * 64 + lane;
       if (u * 64 < nmask * Sh::C4 && it < nmask * Sh::C4) {
+        if constexpr (GATED) {  // both heads of the pair write the same zero row of y
+          const int hh = H / 2;
+          const int64_t off = ((static_cast<int64_t>(b) * N + site[u]) * hh + h % hh) * D + (it % Sh::C4) * 4;
+          store4<F32>(p.out, off, 0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+          for (int t = 0; t < T; ++t) store4<F32>(p.tout, t * p.y_tstride + off, 0.f, 0.f, 0.f, 0.f);
+          continue;
+        }
         const int64_t off = bnhd(b, site[u], h, N, H, D) + (it % Sh::C4) * 4;
         if constexpr (!GIVEN_LSE) store4<F32>(p.out, off, 0.f, 0.f, 0.f, 0.f);
 #pragma unroll
@@ -409,7 +433,12 @@ __device__ __forceinline__ void settle_q(QSet<D, T>& qs) {
 // pf() issues the next item's query prefetch; it runs after this tile's own global loads
 // (bias) are issued, so waiting for those never waits for the prefetch. sq() settles
 // the prefetch before this tile's stores, so the next period never waits for them.
-template <int D, int T, bool GIVEN_LSE, bool HAS_E, int NJ, class PF, class SQ>
+// ROLE 0: plain item (out, lse, tout). Gated head collapse (out = y, tout = its tangents,
+// layout [B, N, H/2, D]): ROLE 1, the gate head g, writes sigma(g) and sigma(g)(1 - sigma(g))
+// gdot to its rows of y and tout; ROLE 2, the value head v of the same pair (the next item
+// of the same workgroup, same tile and lane), reads them back and writes
+// y = sigma(g) v, ydot = sigma'(g) gdot v + sigma(g) vdot.
+template <int D, int T, bool GIVEN_LSE, bool HAS_E, int NJ, int ROLE, class PF, class SQ>
 __device__ __forceinline__ void pc_tile(const FwdParams& p, const char* buf, const int16_t* slot_perm,
                                         const QSet<D, T>& qs, int tile, PF&& pf, SQ&& sq) {
   using Sh = PcShape<D, T>;
@@ -452,6 +481,34 @@ __device__ __forceinline__ void pc_tile(const FwdParams& p, const char* buf, con
           etv[t][jt][r] = buf_load1(et_rs, eo);
         }
       }
+  }
+  // ---- value head of a gated pair: the gate terms this lane stored one item earlier ----
+  static_assert(ROLE == 0 || !GIVEN_LSE, "the gated collapse computes the forward");
+  const int hh = H / 2;
+  const int64_t ywrow = static_cast<int64_t>(N) * hh * D;  // floats of y per walker
+  const int ybytes = static_cast<int>(ywrow * 4);
+  const int ybase = (qsite * hh + (h % (hh > 0 ? hh : 1))) * D;
+  auto yoff = [&](int dt) {
+    const int d0 = dt * 16 + 4 * g;
+    return (qvalid && (D % 16 == 0 || d0 < D)) ? (ybase + d0) * 4 : ybytes;
+  };
+  float gsv[ROLE == 2 ? DT : 1][4], gdv[ROLE == 2 ? TT : 1][ROLE == 2 ? DT : 1][4];
+  if constexpr (ROLE == 2) {
+    const __amdgpu_buffer_rsrc_t y_rs = make_rsrc(static_cast<float*>(p.out) + b * ywrow, ybytes);
+#pragma unroll
+    for (int dt = 0; dt < DT; ++dt) {
+      const float4 u = buf_load4(y_rs, yoff(dt));
+      gsv[dt][0] = u.x, gsv[dt][1] = u.y, gsv[dt][2] = u.z, gsv[dt][3] = u.w;
+    }
+#pragma unroll
+    for (int t = 0; t < T; ++t) {
+      const __amdgpu_buffer_rsrc_t t_rs = make_rsrc(static_cast<float*>(p.tout) + t * p.y_tstride + b * ywrow, ybytes);
+#pragma unroll
+      for (int dt = 0; dt < DT; ++dt) {
+        const float4 u = buf_load4(t_rs, yoff(dt));
+        gdv[t][dt][0] = u.x, gdv[t][dt][1] = u.y, gdv[t][dt][2] = u.z, gdv[t][dt][3] = u.w;
+      }
+    }
   }
   pf();
 
@@ -660,6 +717,32 @@ __device__ __forceinline__ void pc_tile(const FwdParams& p, const char* buf, con
   sq();
 
   // ---- stores: unconditional, invalid lanes past the walker's last record ------------
+  if constexpr (ROLE != 0) {
+    const __amdgpu_buffer_rsrc_t y_rs = make_rsrc(static_cast<float*>(p.out) + b * ywrow, ybytes);
+    float sg[DT][4];
+#pragma unroll
+    for (int dt = 0; dt < DT; ++dt) {
+#pragma unroll
+      for (int r = 0; r < 4; ++r)
+        sg[dt][r] = ROLE == 1 ? __builtin_amdgcn_rcpf(1.f + fast_exp2(-kLog2e * ov[dt][r])) : gsv[dt][r] * ov[dt][r];
+      buf_store4(y_rs, yoff(dt), sg[dt][0], sg[dt][1], sg[dt][2], sg[dt][3]);
+    }
+#pragma unroll
+    for (int t = 0; t < T; ++t) {
+      const __amdgpu_buffer_rsrc_t t_rs = make_rsrc(static_cast<float*>(p.tout) + t * p.y_tstride + b * ywrow, ybytes);
+#pragma unroll
+      for (int dt = 0; dt < DT; ++dt) {
+        float tv[4];
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const float od = fmaf(-mut[t], ov[dt][r], fmaf(at[t][dt][r], inv_ln2, ct[t][dt][r] * inv));
+          tv[r] = ROLE == 1 ? sg[dt][r] * (1.f - sg[dt][r]) * od : fmaf(gdv[t][dt][r], ov[dt][r], gsv[dt][r] * od);
+        }
+        buf_store4(t_rs, yoff(dt), tv[0], tv[1], tv[2], tv[3]);
+      }
+    }
+    return;
+  }
   const int64_t wrow = static_cast<int64_t>(N) * H * D;  // floats per walker
   const int obytes = static_cast<int>(wrow * 4);
   const int obase = (qsite * H + h) * D;
@@ -692,7 +775,7 @@ __device__ __forceinline__ void pc_tile(const FwdParams& p, const char* buf, con
   }
 }
 
-template <int D, int T, bool GIVEN_LSE, bool HAS_E>
+template <int D, int T, bool GIVEN_LSE, bool HAS_E, bool GATED>
 __device__ __forceinline__ void pc_consumer(const FwdParams& p, const char* lds, const ItemSeq& seq, int cnt) {
   using Sh = PcShape<D, T>;
   const int wave = threadIdx.x >> 6;
@@ -716,7 +799,8 @@ __device__ __forceinline__ void pc_consumer(const FwdParams& p, const char* lds,
   };
 
   // Item k with this wave's query fragments qs; the next item's go into nq_set.
-  auto compute = [&](const QSet<D, T>& qs, QSet<D, T>& nx, int k) {
+  auto compute = [&](auto role, const QSet<D, T>& qs, QSet<D, T>& nx, int k) {
+    constexpr int R = decltype(role)::value;
     const char* buf = lds + (k & 1) * Sh::BUF;
     const int nq = pc_nq(qs.n_phys, km, N);
     const int nk = pc_nk(qs.n_phys, km, N);
@@ -725,10 +809,10 @@ __device__ __forceinline__ void pc_consumer(const FwdParams& p, const char* lds,
     const int16_t* sp = slot_perm(k);
     if (wave * 16 < nq) {
       switch ((nk + 15) >> 4) {
-        case 1: pc_tile<D, T, GIVEN_LSE, HAS_E, 1>(p, buf, sp, qs, wave, pf, sq); break;
-        case 2: pc_tile<D, T, GIVEN_LSE, HAS_E, 2>(p, buf, sp, qs, wave, pf, sq); break;
-        case 3: pc_tile<D, T, GIVEN_LSE, HAS_E, 3>(p, buf, sp, qs, wave, pf, sq); break;
-        default: pc_tile<D, T, GIVEN_LSE, HAS_E, 4>(p, buf, sp, qs, wave, pf, sq); break;
+        case 1: pc_tile<D, T, GIVEN_LSE, HAS_E, 1, R>(p, buf, sp, qs, wave, pf, sq); break;
+        case 2: pc_tile<D, T, GIVEN_LSE, HAS_E, 2, R>(p, buf, sp, qs, wave, pf, sq); break;
+        case 3: pc_tile<D, T, GIVEN_LSE, HAS_E, 3, R>(p, buf, sp, qs, wave, pf, sq); break;
+        default: pc_tile<D, T, GIVEN_LSE, HAS_E, 4, R>(p, buf, sp, qs, wave, pf, sq); break;
       }
     } else {
       pf();
@@ -740,10 +824,10 @@ __device__ __forceinline__ void pc_consumer(const FwdParams& p, const char* lds,
       QSet<D, T> q3;
       pc_load_q<D, T, GIVEN_LSE>(p, q3, qs.b, qs.h, qs.n_phys, sp, 3);
       switch ((nk + 15) >> 4) {
-        case 1: pc_tile<D, T, GIVEN_LSE, HAS_E, 1>(p, buf, sp, q3, 3, [] {}, [] {}); break;
-        case 2: pc_tile<D, T, GIVEN_LSE, HAS_E, 2>(p, buf, sp, q3, 3, [] {}, [] {}); break;
-        case 3: pc_tile<D, T, GIVEN_LSE, HAS_E, 3>(p, buf, sp, q3, 3, [] {}, [] {}); break;
-        default: pc_tile<D, T, GIVEN_LSE, HAS_E, 4>(p, buf, sp, q3, 3, [] {}, [] {}); break;
+        case 1: pc_tile<D, T, GIVEN_LSE, HAS_E, 1, R>(p, buf, sp, q3, 3, [] {}, [] {}); break;
+        case 2: pc_tile<D, T, GIVEN_LSE, HAS_E, 2, R>(p, buf, sp, q3, 3, [] {}, [] {}); break;
+        case 3: pc_tile<D, T, GIVEN_LSE, HAS_E, 3, R>(p, buf, sp, q3, 3, [] {}, [] {}); break;
+        default: pc_tile<D, T, GIVEN_LSE, HAS_E, 4, R>(p, buf, sp, q3, 3, [] {}, [] {}); break;
       }
     }
     __builtin_amdgcn_s_waitcnt(kWaitLgkm0);
@@ -756,37 +840,39 @@ __device__ __forceinline__ void pc_consumer(const FwdParams& p, const char* lds,
     seq.bh(0, b, h);
     pc_load_q<D, T, GIVEN_LSE>(p, qa, b, h, slot_n(0), slot_perm(0), wave);
   }
+  // Gated: cnt is even, so item k (even) is the gate head and k + 1 the value head.
   for (int k = 0; k < cnt; k += 2) {
-    compute(qa, qb, k);
+    compute(std::integral_constant<int, GATED ? 1 : 0>{}, qa, qb, k);
     wg_barrier();
     if (k + 1 >= cnt) break;
-    compute(qb, qa, k + 1);
+    compute(std::integral_constant<int, GATED ? 2 : 0>{}, qb, qa, k + 1);
     wg_barrier();
   }
 }
 
-template <int D, int T, bool GIVEN_LSE, bool HAS_E>
+template <int D, int T, bool GIVEN_LSE, bool HAS_E, bool GATED>
 __global__ void __launch_bounds__(256, 2) mhsea_fwd_pc_kernel(const FwdParams p) {
   using Sh = PcShape<D, T>;
   extern __shared__ float4 smem4[];
   char* const lds = reinterpret_cast<char*>(smem4);
-  const uint32_t nitems = static_cast<uint32_t>(p.B) * static_cast<uint32_t>(p.H);
+  const uint32_t half = GATED ? static_cast<uint32_t>(p.H) / 2 : 0u;
+  const uint32_t nunits = static_cast<uint32_t>(p.B) * (GATED ? half : static_cast<uint32_t>(p.H));
   const uint32_t G = gridDim.x;
   const uint32_t L = static_cast<uint32_t>(xcd_logical_block(blockIdx.x, G));
-  if (L >= nitems) return;  // workgroup-uniform
-  const ItemSeq seq{L, G, nitems, static_cast<uint32_t>(p.H)};
-  const int cnt = static_cast<int>((nitems - L + G - 1) / G);
+  if (L >= nunits) return;  // workgroup-uniform
+  const ItemSeq seq{L, G, nunits, static_cast<uint32_t>(p.H), half};
+  const int cnt = static_cast<int>((nunits - L + G - 1) / G) * (GATED ? 2 : 1);
   if ((threadIdx.x >> 6) == kProducerWave)
-    pc_producer<D, T, GIVEN_LSE>(p, lds, seq, cnt);
+    pc_producer<D, T, GIVEN_LSE, GATED>(p, lds, seq, cnt);
   else
-    pc_consumer<D, T, GIVEN_LSE, HAS_E>(p, lds, seq, cnt);
+    pc_consumer<D, T, GIVEN_LSE, HAS_E, GATED>(p, lds, seq, cnt);
   (void)Sh::LDS;
 }
 
-template <int D, int T, bool GIVEN_LSE, bool HAS_E>
+template <int D, int T, bool GIVEN_LSE, bool HAS_E, bool GATED>
 hipError_t launch_pc_t(const FwdParams& p, hipStream_t stream) {
   using Sh = PcShape<D, T>;
-  auto kern = mhsea_fwd_pc_kernel<D, T, GIVEN_LSE, HAS_E>;
+  auto kern = mhsea_fwd_pc_kernel<D, T, GIVEN_LSE, HAS_E, GATED>;
   const size_t lds = Sh::LDS;
   if (lds > 64 * 1024) {
     hipError_t err = hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
@@ -807,9 +893,9 @@ hipError_t launch_pc_t(const FwdParams& p, hipStream_t stream) {
   int cus = 0;
   hipError_t err = device_cu_count(&cus);
   if (err != hipSuccess) return err;
-  const int64_t nitems = static_cast<int64_t>(p.B) * p.H;
+  const int64_t nunits = static_cast<int64_t>(p.B) * (GATED ? p.H / 2 : p.H);
   int64_t grid = static_cast<int64_t>(cus) * per_cu;
-  if (grid > nitems) grid = nitems;
+  if (grid > nunits) grid = nunits;
   hipLaunchKernelGGL(kern, dim3(static_cast<unsigned>(grid)), dim3(256), lds, stream, p);
   return hipGetLastError();
 }
@@ -823,8 +909,14 @@ constexpr bool pc_shape_ok() {
 template <int D, int T, bool GIVEN_LSE>
 hipError_t dispatch_e(const FwdParams& p, hipStream_t stream) {
   if constexpr (pc_shape_ok<D, T>()) {
-    if (p.e != nullptr || p.et != nullptr) return launch_pc_t<D, T, GIVEN_LSE, true>(p, stream);
-    return launch_pc_t<D, T, GIVEN_LSE, false>(p, stream);
+    const bool e = p.e != nullptr || p.et != nullptr;
+    if constexpr (!GIVEN_LSE) {
+      if (p.gated) return e ? launch_pc_t<D, T, false, true, true>(p, stream) : launch_pc_t<D, T, false, false, true>(p, stream);
+    } else {
+      if (p.gated) return hipErrorInvalidValue;
+    }
+    if (e) return launch_pc_t<D, T, GIVEN_LSE, true, false>(p, stream);
+    return launch_pc_t<D, T, GIVEN_LSE, false, false>(p, stream);
   }
   return hipErrorInvalidValue;
 }

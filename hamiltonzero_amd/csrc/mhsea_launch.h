@@ -30,6 +30,11 @@ struct FwdParams {
   int key_mask;  // 1: reference_edge_attention masking (keys only)
   float masked_lse;
   int force_generic;  // 1: always use the LDS-streaming kernel
+  // 1: gated head collapse (producer/consumer kernel only): out is y [B, N, H/2, D] =
+  // sigmoid(O[:, :, h]) * O[:, :, h + H/2], tout its tangents [T, B, N, H/2, D] with
+  // y_tstride elements between directions; lse is not written
+  int gated;
+  int64_t y_tstride;
 };
 
 struct BwdParams {

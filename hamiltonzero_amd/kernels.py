@@ -220,6 +220,52 @@ def mhsea_fwd_jvp(
     return out, lse, (tout if batched else tout[0])
 
 
+def mhsea_fwd_jvp_gated(
+    q: Tensor,
+    k: Tensor,
+    v: Tensor,
+    mask: Tensor,
+    qt: Optional[Tensor] = None,
+    kt: Optional[Tensor] = None,
+    vt: Optional[Tensor] = None,
+    e: Optional[Tensor] = None,
+    et: Optional[Tensor] = None,
+    *,
+    scale: float = 1.0,
+    key_mask: bool = False,
+    e_layout: str = "qhk",
+) -> Tuple[Tensor, Optional[Tensor]]:
+    """Fused forward (+ tangents) with the trunk's sigmoid-gate head collapse in the epilogue
+    (``trunk.py:134-137``): head h < H/2 gates head h + H/2. Returns ``(y, ty)`` with
+    ``y = sigmoid(out[:, :, :H/2]) * out[:, :, H/2:]`` of shape ``[B, N, H/2, D]`` and its
+    forward-mode tangents (``[T, B, N, H/2, D]`` for batched tangents, ``[B, N, H/2, D]``
+    for one, None when no tangent is given). Serves fp32, N <= 64, D in {8, 16, 32}, even H,
+    at most two tangent directions."""
+    B, N, H, D = _check_primals(q, k, v, mask, e, e_layout)
+    if q.dtype != torch.float32:
+        raise TypeError(f"the gated collapse computes in float32, got {q.dtype}")
+    if H % 2:
+        raise ValueError(f"the gated collapse pairs head h with h + H/2: H must be even, got {H}")
+    e_shape = (B, N, H, N) if e_layout == "qhk" else (B, N, N, H)
+    if all(t is None for t in (qt, kt, vt, et)):
+        T, batched = 0, False
+    else:
+        batched = any(t is not None and t.dim() == 5 for t in (qt, kt, vt)) or (et is not None and et.dim() == 5)
+        qt, kt, et, vt, T = _tangents(q, e_shape, qt, kt, et, vt)
+    q, k, v, e = _c(q), _c(k), _c(v), _c(e)
+    m = _mask_u8(mask, q.device)
+    y = torch.empty((B, N, H // 2, D), dtype=q.dtype, device=q.device)
+    ty = torch.empty((T, B, N, H // 2, D), dtype=q.dtype, device=q.device) if T else None
+    _native.check(
+        _native.lib().hz_mhsea_fwd_jvp_gated(
+            _stream(q.device), _ptr(q), _ptr(k), _ptr(e), _ptr(v), _ptr(m),
+            _ptr(qt), _ptr(kt), _ptr(et), _ptr(vt), T, _ptr(y), _ptr(ty),
+            B, N, H, D, float(scale), _flags(key_mask, e_layout, False),
+        )
+    )
+    return y, (None if ty is None else (ty if batched else ty[0]))
+
+
 def mhsea_bwd(
     q: Tensor,
     k: Tensor,

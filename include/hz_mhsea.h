@@ -132,6 +132,27 @@ int hz_mhsea_fwd_jvp(hipStream_t stream,
                      int dtype, float scale, int flags);
 
 /*
+ * Fused forward + T tangents with the trunk's sigmoid-gate head collapse in the epilogue.
+ * Replaces the caller-side code after the attention call in trunk.py:134-137
+ *     gate = out[:, :H/2], value = out[:, H/2:], y = sigmoid(gate) * value
+ * together with its forward-mode tangent
+ *     ydot[t] = sigmoid(gate) (1 - sigmoid(gate)) gatedot[t] * value + sigmoid(gate) valuedot[t]
+ * where out and tout[t] are what hz_mhsea_fwd_jvp computes. Head h < H/2 is the gate of
+ * head h + H/2. Writes y [B, N, H/2, D] and ty [T, B, N, H/2, D] (masked query rows 0);
+ * out, lse and the per-head tangents never reach memory.
+ * Served shapes (the producer/consumer kernel): fp32, N <= 64, D in {8, 16, 32}, H even,
+ * 0 <= T <= 2 (at D = 32 two directions run as two passes); others return HZ_EINVAL. Required: q, k, v, mask, y, and ty when T >= 1.
+ * Optional: e, qt, kt, et, vt (tangent strides B*N*H*D; ty's stride is B*N*(H/2)*D).
+ */
+int hz_mhsea_fwd_jvp_gated(hipStream_t stream,
+                           const void* q, const void* k, const void* e, const void* v,
+                           const uint8_t* mask,
+                           const void* qt, const void* kt, const void* et, const void* vt,
+                           int64_t T, void* y, void* ty,
+                           int64_t B, int64_t N, int64_t H, int64_t D,
+                           float scale, int flags);
+
+/*
  * Reverse mode: cotangents of (q, k, e, v) for the upstream cotangent dout. Replaces the
  * transpose rule _inner_transpose (mhsea_tuned.py:206-221 -> mhsea_backward,
  * custom_gradients.py:78-228 -> mhsea_q_vjp_kernel :231-285, mhsea_kv_vjp_kernel

@@ -173,6 +173,29 @@ def vjp(q, k, e, v, mask, dout, *, scale=1.0, key_mask=False, e_layout="qhk"):
     return dq, dk, _e_back(ds, e_layout), dv
 
 
+def gate_collapse(out):
+    """The trunk's sigmoid-gate head collapse after the attention call (trunk.py:134-137):
+    head h < H/2 of ``out [B, N, H, D]`` gates head h + H/2,
+    ``y = sigmoid(out[:, :, :H/2]) * out[:, :, H/2:]`` of shape [B, N, H/2, D]."""
+    out = _f64(out)
+    hh = out.shape[2] // 2
+    return out[:, :, hh:] / (1.0 + np.exp(-out[:, :, :hh]))
+
+
+def gated_fwd_jvp(q, k, e, v, mask, qt, kt, et, vt, *, scale=1.0, key_mask=False, e_layout="qhk"):
+    """(y, ydot): ``gate_collapse`` of ``fwd``'s out and its forward-mode tangent along
+    (qt, kt, et, vt), ``ydot = s (1 - s) gdot value + s vdot`` with ``s = sigmoid(gate)`` and
+    (gdot, vdot) the gate / value heads of ``jvp``'s tangent (the chain rule through
+    trunk.py:136)."""
+    out, _ = fwd(q, k, e, v, mask, scale=scale, key_mask=key_mask, e_layout=e_layout)
+    tout = jvp(q, k, e, v, mask, qt, kt, et, vt, scale=scale, key_mask=key_mask, e_layout=e_layout)
+    hh = out.shape[2] // 2
+    s = 1.0 / (1.0 + np.exp(-out[:, :, :hh]))
+    y = s * out[:, :, hh:]
+    ydot = s * (1.0 - s) * tout[:, :, :hh] * out[:, :, hh:] + s * tout[:, :, hh:]
+    return y, ydot
+
+
 def reference_edge_attention(Q, K, V, edge_bias, mask):
     """Per-system jnp op (pallas_attention.py:22-37): [n,h,d], [n,n,h], [n] -> [n,h,d]."""
     d = np.asarray(Q).shape[-1]

@@ -147,3 +147,33 @@ def test_rect_rejects_bad_arguments(lib):
         assert call(**over) == code, over
         assert needle in lib.hz_last_error().decode(), over
     assert len(lib.hz_rect_attention_fwd.argtypes) == 13
+
+
+def test_gated_rejects_bad_arguments(lib):
+    # stream, q, k, e, v, mask, qt, kt, et, vt, T, y, ty, B, N, H, D, scale, flags
+    names = ["stream", "q", "k", "e", "v", "mask", "qt", "kt", "et", "vt", "T", "y", "ty",
+             "B", "N", "H", "D", "scale", "flags"]
+    base = [None, A, A, None, A, A, None, None, None, None, 1, A, A, 2, 64, 8, 32, 0.125, 0]
+
+    def call(**over):
+        args = list(base)
+        for key, val in over.items():
+            args[names.index(key)] = val
+        return lib.hz_mhsea_fwd_jvp_gated(*args)
+
+    cases = [
+        (dict(H=7), _native.HZ_EINVAL, "H must be even"),
+        (dict(T=3), _native.HZ_EINVAL, "T must be in [0, 2]"),
+        (dict(D=64), _native.HZ_EINVAL, "serves fp32, N <= 64"),
+        (dict(N=65), _native.HZ_EINVAL, "serves fp32, N <= 64"),
+        (dict(D=24), _native.HZ_EINVAL, "head dimension"),
+        (dict(flags=4), _native.HZ_EINVAL, "HZ_FLAG_GENERIC"),
+        (dict(y=None), _native.HZ_ENULL, "y must not be NULL"),
+        (dict(ty=None), _native.HZ_ENULL, "ty must not be NULL"),
+        (dict(qt=A + 4), _native.HZ_EALIGN, "qt"),
+        (dict(scale=float("nan")), _native.HZ_EINVAL, "scale"),
+    ]
+    for over, code, needle in cases:
+        assert call(**over) == code, over
+        assert needle in lib.hz_last_error().decode(), over
+    assert len(lib.hz_mhsea_fwd_jvp_gated.argtypes) == 19

@@ -1,0 +1,107 @@
+"""GPU parity of the gated head collapse (hz_mhsea_fwd_jvp_gated) against the float64 oracle.
+
+The fused kernel's y = sigmoid(gate) * value and its tangents are compared with
+``oracle.mhsea_oracle.gated_fwd_jvp`` (pinned in tests/test_gated_oracle.py) on seeded
+inputs, over T in {0, 1, 2}, D in {8, 16, 32}, prefix / scattered / empty masks, the key-mask
+mode, bias in both layouts, and grids where one workgroup walks several head pairs; and
+against the unfused composition (hz_mhsea_fwd_jvp, then the collapse in torch) at c2's shape.
+Tolerance: max-norm relative error <= 1e-5 (float32).
+"""
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import mhsea_oracle as O
+
+pytestmark = pytest.mark.gpu
+
+TOL = 1e-5
+
+
+def _say(msg):
+    print(f"[case] {msg}", flush=True)
+
+
+def rel(a, b):
+    a = np.asarray(a, dtype=np.float64)
+    b = np.asarray(b, dtype=np.float64)
+    return float(np.max(np.abs(a - b)) / max(np.max(np.abs(b)), 1e-30))
+
+
+def make(seed, B, N, H, D, T, mask_kind, with_e, e_layout):
+    rng = np.random.default_rng(seed)
+    shape = (B, N, H, D)
+    q, k, v = (rng.standard_normal(shape, dtype=np.float32) * np.float32(D ** -0.5) for _ in range(3))
+    eshape = (B, N, H, N) if e_layout == "qhk" else (B, N, N, H)
+    e = rng.standard_normal(eshape, dtype=np.float32) * np.float32(0.5) if with_e else None
+    tq, tk, tv = (rng.standard_normal((max(T, 1), *shape), dtype=np.float32) for _ in range(3))
+    te = rng.standard_normal((max(T, 1), *eshape), dtype=np.float32) if with_e else None
+    mask = np.zeros((B, N), dtype=bool)
+    for b in range(B):
+        n = int(rng.integers(0, N + 1)) if mask_kind == "counts" else max(1, (9 * N) // 16)
+        mask[b, np.arange(n) if mask_kind == "prefix" else rng.permutation(N)[:n]] = True
+    return q, k, v, e, mask, tq, tk, tv, te
+
+
+CASES = [
+    # seed, B, N, H, D, T, mask, key_mask, e, e_layout
+    (1, 64, 64, 8, 32, 1, "prefix", False, False, "qhk"),
+    (2, 37, 64, 8, 32, 2, "scattered", False, True, "qhk"),
+    (3, 20, 40, 4, 16, 1, "counts", False, True, "qkh"),
+    (4, 50, 64, 2, 8, 0, "scattered", False, False, "qhk"),
+    (5, 9, 17, 6, 32, 2, "counts", True, True, "qhk"),
+    (6, 300, 64, 8, 32, 1, "scattered", False, False, "qhk"),
+    (7, 3, 8, 4, 16, 1, "prefix", False, True, "qhk"),
+    (8, 11, 64, 4, 32, 0, "counts", True, False, "qhk"),
+]
+
+
+@pytest.mark.parametrize("case", CASES, ids=["s{}_B{}_N{}_H{}_D{}_T{}_{}{}{}{}".format(
+    c[0], c[1], c[2], c[3], c[4], c[5], c[6], "_keymask" if c[7] else "", "_e" if c[8] else "", c[9] if c[8] else "")
+    for c in CASES])
+def test_gated_matches_oracle(case):
+    from hamiltonzero_amd import kernels
+
+    seed, B, N, H, D, T, mask_kind, key_mask, with_e, e_layout = case
+    _say(f"gated {case}")
+    q, k, v, e, mask, tq, tk, tv, te = make(seed, B, N, H, D, T, mask_kind, with_e, e_layout)
+    dev = lambda x: None if x is None else torch.from_numpy(x).cuda()  # noqa: E731
+    scale = D ** -0.5
+    kw = dict(scale=scale, key_mask=key_mask, e_layout=e_layout)
+    if T == 0:
+        y, ty = kernels.mhsea_fwd_jvp_gated(dev(q), dev(k), dev(v), dev(mask), e=dev(e), **kw)
+        assert ty is None
+    else:
+        y, ty = kernels.mhsea_fwd_jvp_gated(dev(q), dev(k), dev(v), dev(mask), dev(tq[:T]), dev(tk[:T]), dev(tv[:T]),
+                                            e=dev(e), et=None if te is None else dev(te[:T]), **kw)
+    torch.cuda.synchronize()
+    assert tuple(y.shape) == (B, N, H // 2, D)
+    for t in range(max(T, 1)):
+        ey, eyd = O.gated_fwd_jvp(q, k, e, v, mask, tq[t], tk[t], None if te is None else te[t], tv[t], **kw)
+        if t == 0:
+            assert rel(y.cpu().numpy(), ey) <= TOL, "y"
+            if not key_mask:
+                assert np.all(y.cpu().numpy()[~mask] == 0.0)
+        if T:
+            assert rel(ty[t].cpu().numpy(), eyd) <= TOL, f"ydot {t}"
+
+
+def test_gated_equals_unfused_composition_at_c2_shape():
+    from hamiltonzero_amd import kernels
+
+    _say("gated vs unfused at [1024, 64, 8, 32], 36/64")
+    B, N, H, D = 1024, 64, 8, 32
+    g = torch.Generator(device="cuda").manual_seed(1)
+    q, k, v = (torch.randn(B, N, H, D, device="cuda", generator=g) * D ** -0.5 for _ in range(3))
+    qt, kt, vt = (torch.randn(B, N, H, D, device="cuda", generator=g) for _ in range(3))
+    mask = torch.zeros(B, N, dtype=torch.bool, device="cuda")
+    mask[:, :36] = True
+    y, ty = kernels.mhsea_fwd_jvp_gated(q, k, v, mask, qt, kt, vt, scale=D ** -0.5)
+    out, _, tout = kernels.mhsea_fwd_jvp(q, k, v, mask, qt, kt, vt, scale=D ** -0.5)
+    s = torch.sigmoid(out[:, :, : H // 2])
+    want_y = s * out[:, :, H // 2:]
+    want_ty = s * (1 - s) * tout[:, :, : H // 2] * out[:, :, H // 2:] + s * tout[:, :, H // 2:]
+    torch.cuda.synchronize()
+    assert rel(y.cpu().numpy(), want_y.cpu().numpy()) <= TOL
+    assert rel(ty.cpu().numpy(), want_ty.cpu().numpy()) <= TOL
