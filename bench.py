@@ -26,6 +26,8 @@ if ROOT not in sys.path:
     sys.path.insert(0, ROOT)
 
 METRIC = "fwd+JVP attention walkers/sec at B=1024,L=64; % of MFMA/HBM roofline"
+GATE_METRIC = ("fwd+JVP attention with the sigmoid-gate head collapse fused, walkers/sec at B=1024,L=64; "
+               "% of MFMA/HBM roofline")
 HBM_PEAK_GBS = 8000.0
 FP32_PEAK_TFLOPS = 157.3
 BF16_PEAK_TFLOPS = 2516.6
@@ -41,6 +43,12 @@ CONFIGS = {
            "large-N forward + JVP, fp32, [512,256,8,64], 225/256 physical sites (15x15)"),
     "c5": ("fwd_jvp", 128, 1024, 16, 64, 1000, 2, "bf16", 4,
            "large-N stress forward + 2 JVP directions, bf16 I/O, [128,1024,16,64], 1000/1024 sites"),
+    # The caller-side epilogue of the trunk (trunk.py:134-137) fused into c2's kernel: head h
+    # gates head h + H/2, and only y = sigmoid(gate) * value and its tangent are written.
+    # Reported beside the hot path, never as the default line.
+    "gate": ("fwd_jvp_gated", 1024, 64, 8, 32, 36, 1, "f32", 1,
+             "c2's forward + JVP with the sigmoid-gate head collapse fused, fp32, [1024,64,8,32] -> "
+             "y, ydot [1024,64,4,32], 36/64 physical sites"),
     # The large-N evaluation forward (noncausal_bias_mha via pallas_rectangular_edge_attention):
     # one system, all queries against all keys, dense [Nq, Nk, H] bias. Not one of c1-c5:
     # reported beside the hot path, never as the default line.
@@ -156,13 +164,15 @@ def algorithmic(work, B, N, H, D, n_phys, T, esize):
         n_in, n_out, g_mult, lse_b = 3, 1, 2, 0
     elif work == "fwd_jvp":
         n_in, n_out, g_mult, lse_b = 3 + 3 * T, 1 + T, 2 + 4 * T, 0
+    elif work == "fwd_jvp_gated":  # outputs are y and its T tangents, each half a [B,N,H,D] tensor
+        n_in, n_out, g_mult, lse_b = 3 + 3 * T, (1 + T) / 2, 2 + 4 * T, 0
     elif work == "fwd_vjp":
         # fwd: q,k,v in, out + lse out; bwd: q,k,v,out,dout + lse in, dq,dk,dv out
         n_in, n_out, g_mult, lse_b = 3 + 5, 1 + 3, 6, 2 * N * H * 4
     else:
         raise ValueError(work)
-    padded_bytes = B * (N * rowb * (n_in + n_out) + N + lse_b)
-    eff_bytes = B * (n_phys * rowb * n_in + N * rowb * n_out + N + lse_b)
+    padded_bytes = int(B * (N * rowb * (n_in + n_out) + N + lse_b))
+    eff_bytes = int(B * (n_phys * rowb * n_in + N * rowb * n_out + N + lse_b))
     padded_flops = B * H * g_mult * 2 * N * N * D
     eff_flops = B * H * g_mult * 2 * n_phys * n_phys * D
     return dict(padded_bytes=padded_bytes, eff_bytes=eff_bytes, padded_flops=padded_flops,
@@ -281,7 +291,7 @@ def main(argv=None):
         def step():
             _native.check(lib.hz_mhsea_fwd(s, P(q), P(k), None, P(v), P(mask), P(out), None,
                                            B, N, H, D, hz_dtype, 1.0, fl))
-    elif work == "fwd_jvp":
+    elif work in ("fwd_jvp", "fwd_jvp_gated"):
         qt = torch.stack([t[0] for t in tans]).contiguous()
         kt = torch.stack([t[1] for t in tans]).contiguous()
         vt = torch.stack([t[2] for t in tans]).contiguous()
@@ -291,6 +301,15 @@ def main(argv=None):
         def step():
             _native.check(lib.hz_mhsea_fwd_jvp(s, P(q), P(k), None, P(v), P(mask), P(qt), P(kt), None, P(vt), T,
                                                P(out), None, P(tout), B, N, H, D, hz_dtype, 1.0, fl))
+
+        if work == "fwd_jvp_gated":
+            y = torch.empty((B, N, H // 2, D), dtype=tdt, device=dev)
+            ty = torch.empty((T, B, N, H // 2, D), dtype=tdt, device=dev)
+            del out, tout
+
+            def step():
+                _native.check(lib.hz_mhsea_fwd_jvp_gated(s, P(q), P(k), None, P(v), P(mask), P(qt), P(kt), None,
+                                                         P(vt), T, P(y), P(ty), B, N, H, D, 1.0, 0))
     else:
         lse = torch.empty((B, N, H), dtype=torch.float32, device=dev)
         dq, dk, dv = (torch.empty(shape, dtype=tdt, device=dev) for _ in range(3))
@@ -325,7 +344,7 @@ def main(argv=None):
         from oracle import cpu_baseline
 
         threads = int(os.environ.get("OMP_NUM_THREADS", os.cpu_count() or 1))
-        sample = {"c1": 256, "c2": 64, "c3": 32, "c4": 4, "c5": 1}[args.config]
+        sample = {"c1": 256, "c2": 64, "c3": 32, "c4": 4, "c5": 1, "gate": 64}[args.config]
         r = cpu_baseline.time_walkers_per_s(work, sample, N, H, D, n_phys, seed, T=max(T, 1),
                                             bf16_inputs=(dtype == "bf16"), budget_s=args.cpu_budget,
                                             threads=threads)
@@ -339,7 +358,7 @@ def main(argv=None):
         }
 
     line = {
-        "metric": METRIC,
+        "metric": GATE_METRIC if work == "fwd_jvp_gated" else METRIC,
         "value": walkers_s,
         "unit": "walkers/s",
         "n_gpus": 1,

@@ -252,6 +252,7 @@ __device__ __forceinline__ void pc_producer(const FwdParams& p, char* lds, const
   constexpr int NMI = Sh::C4;  // passes for N = 64 (64 rows x C4 float4 / 64 lanes)
   auto masked_rows = [&](int k, const PcSites& st) {
     if (km) return;
+    if (GATED && (k & 1) == 0) return;  // the value head (odd k) writes the pair's zero rows
     int b, h;
     seq.bh(k, b, h);
     const int nmask = N - st.n_phys;
@@ -262,7 +263,7 @@ __device__ __forceinline__ void pc_producer(const FwdParams& p, char* lds, const
     for (int u = 0; u < NMI; ++u) {
       const int it = u * 64 + lane;
       if (u * 64 < nmask * Sh::C4 && it < nmask * Sh::C4) {
-        if constexpr (GATED) {  // both heads of the pair write the same zero row of y
+        if constexpr (GATED) {  // row of y for the pair (b, h - H/2)
           const int hh = H / 2;
           const int64_t off = ((static_cast<int64_t>(b) * N + site[u]) * hh + h % hh) * D + (it % Sh::C4) * 4;
           store4<F32>(p.out, off, 0.f, 0.f, 0.f, 0.f);
@@ -433,14 +434,21 @@ __device__ __forceinline__ void settle_q(QSet<D, T>& qs) {
 // pf() issues the next item's query prefetch; it runs after this tile's own global loads
 // (bias) are issued, so waiting for those never waits for the prefetch. sq() settles
 // the prefetch before this tile's stores, so the next period never waits for them.
+// Gate terms of one 16-query tile, carried in registers from the gate head's item to the
+// value head's (the next item of the same workgroup: same tile, same lane).
+template <int D, int T>
+struct GateRegs {
+  float s[PcShape<D, T>::DT][4];                         // sigma(g)
+  float d[PcShape<D, T>::TT][PcShape<D, T>::DT][4];      // sigma(g) (1 - sigma(g)) gdot[t]
+};
+
 // ROLE 0: plain item (out, lse, tout). Gated head collapse (out = y, tout = its tangents,
-// layout [B, N, H/2, D]): ROLE 1, the gate head g, writes sigma(g) and sigma(g)(1 - sigma(g))
-// gdot to its rows of y and tout; ROLE 2, the value head v of the same pair (the next item
-// of the same workgroup, same tile and lane), reads them back and writes
+// layout [B, N, H/2, D]): ROLE 1, the gate head g, leaves sigma(g) and sigma'(g) gdot in gr
+// and writes nothing; ROLE 2, the value head v of the same pair, writes
 // y = sigma(g) v, ydot = sigma'(g) gdot v + sigma(g) vdot.
 template <int D, int T, bool GIVEN_LSE, bool HAS_E, int NJ, int ROLE, class PF, class SQ>
 __device__ __forceinline__ void pc_tile(const FwdParams& p, const char* buf, const int16_t* slot_perm,
-                                        const QSet<D, T>& qs, int tile, PF&& pf, SQ&& sq) {
+                                        const QSet<D, T>& qs, int tile, PF&& pf, SQ&& sq, GateRegs<D, T>& gr) {
   using Sh = PcShape<D, T>;
   constexpr int DG = Sh::DG, DT = Sh::DT, TT = Sh::TT;
   const int lane = threadIdx.x & 63;
@@ -482,34 +490,7 @@ __device__ __forceinline__ void pc_tile(const FwdParams& p, const char* buf, con
         }
       }
   }
-  // ---- value head of a gated pair: the gate terms this lane stored one item earlier ----
   static_assert(ROLE == 0 || !GIVEN_LSE, "the gated collapse computes the forward");
-  const int hh = H / 2;
-  const int64_t ywrow = static_cast<int64_t>(N) * hh * D;  // floats of y per walker
-  const int ybytes = static_cast<int>(ywrow * 4);
-  const int ybase = (qsite * hh + (h % (hh > 0 ? hh : 1))) * D;
-  auto yoff = [&](int dt) {
-    const int d0 = dt * 16 + 4 * g;
-    return (qvalid && (D % 16 == 0 || d0 < D)) ? (ybase + d0) * 4 : ybytes;
-  };
-  float gsv[ROLE == 2 ? DT : 1][4], gdv[ROLE == 2 ? TT : 1][ROLE == 2 ? DT : 1][4];
-  if constexpr (ROLE == 2) {
-    const __amdgpu_buffer_rsrc_t y_rs = make_rsrc(static_cast<float*>(p.out) + b * ywrow, ybytes);
-#pragma unroll
-    for (int dt = 0; dt < DT; ++dt) {
-      const float4 u = buf_load4(y_rs, yoff(dt));
-      gsv[dt][0] = u.x, gsv[dt][1] = u.y, gsv[dt][2] = u.z, gsv[dt][3] = u.w;
-    }
-#pragma unroll
-    for (int t = 0; t < T; ++t) {
-      const __amdgpu_buffer_rsrc_t t_rs = make_rsrc(static_cast<float*>(p.tout) + t * p.y_tstride + b * ywrow, ybytes);
-#pragma unroll
-      for (int dt = 0; dt < DT; ++dt) {
-        const float4 u = buf_load4(t_rs, yoff(dt));
-        gdv[t][dt][0] = u.x, gdv[t][dt][1] = u.y, gdv[t][dt][2] = u.z, gdv[t][dt][3] = u.w;
-      }
-    }
-  }
   pf();
 
   // Scores are formed in base 2: log2(e) rides on the query scale, so S^T and dS^T leave
@@ -717,16 +698,33 @@ __device__ __forceinline__ void pc_tile(const FwdParams& p, const char* buf, con
   sq();
 
   // ---- stores: unconditional, invalid lanes past the walker's last record ------------
-  if constexpr (ROLE != 0) {
+  if constexpr (ROLE == 1) {
+#pragma unroll
+    for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const float sg = __builtin_amdgcn_rcpf(1.f + fast_exp2(-kLog2e * ov[dt][r]));
+        gr.s[dt][r] = sg;
+#pragma unroll
+        for (int t = 0; t < T; ++t)
+          gr.d[t][dt][r] = sg * (1.f - sg) * fmaf(-mut[t], ov[dt][r], fmaf(at[t][dt][r], inv_ln2, ct[t][dt][r] * inv));
+      }
+    return;
+  }
+  if constexpr (ROLE == 2) {
+    const int hh = H / 2;
+    const int64_t ywrow = static_cast<int64_t>(N) * hh * D;  // floats of y per walker
+    const int ybytes = static_cast<int>(ywrow * 4);
+    const int ybase = (qsite * hh + (h - hh)) * D;
+    auto yoff = [&](int dt) {
+      const int d0 = dt * 16 + 4 * g;
+      return (qvalid && (D % 16 == 0 || d0 < D)) ? (ybase + d0) * 4 : ybytes;
+    };
     const __amdgpu_buffer_rsrc_t y_rs = make_rsrc(static_cast<float*>(p.out) + b * ywrow, ybytes);
-    float sg[DT][4];
 #pragma unroll
-    for (int dt = 0; dt < DT; ++dt) {
-#pragma unroll
-      for (int r = 0; r < 4; ++r)
-        sg[dt][r] = ROLE == 1 ? __builtin_amdgcn_rcpf(1.f + fast_exp2(-kLog2e * ov[dt][r])) : gsv[dt][r] * ov[dt][r];
-      buf_store4(y_rs, yoff(dt), sg[dt][0], sg[dt][1], sg[dt][2], sg[dt][3]);
-    }
+    for (int dt = 0; dt < DT; ++dt)
+      buf_store4(y_rs, yoff(dt), gr.s[dt][0] * ov[dt][0], gr.s[dt][1] * ov[dt][1], gr.s[dt][2] * ov[dt][2],
+                 gr.s[dt][3] * ov[dt][3]);
 #pragma unroll
     for (int t = 0; t < T; ++t) {
       const __amdgpu_buffer_rsrc_t t_rs = make_rsrc(static_cast<float*>(p.tout) + t * p.y_tstride + b * ywrow, ybytes);
@@ -736,7 +734,7 @@ __device__ __forceinline__ void pc_tile(const FwdParams& p, const char* buf, con
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
           const float od = fmaf(-mut[t], ov[dt][r], fmaf(at[t][dt][r], inv_ln2, ct[t][dt][r] * inv));
-          tv[r] = ROLE == 1 ? sg[dt][r] * (1.f - sg[dt][r]) * od : fmaf(gdv[t][dt][r], ov[dt][r], gsv[dt][r] * od);
+          tv[r] = fmaf(gr.d[t][dt][r], ov[dt][r], gr.s[dt][r] * od);
         }
         buf_store4(t_rs, yoff(dt), tv[0], tv[1], tv[2], tv[3]);
       }
@@ -799,6 +797,8 @@ __device__ __forceinline__ void pc_consumer(const FwdParams& p, const char* lds,
   };
 
   // Item k with this wave's query fragments qs; the next item's go into nq_set.
+  // gate terms of this wave's tile and of the fourth tile (consumer 0), gated collapse only
+  GateRegs<D, T> gm, gx;
   auto compute = [&](auto role, const QSet<D, T>& qs, QSet<D, T>& nx, int k) {
     constexpr int R = decltype(role)::value;
     const char* buf = lds + (k & 1) * Sh::BUF;
@@ -809,10 +809,10 @@ __device__ __forceinline__ void pc_consumer(const FwdParams& p, const char* lds,
     const int16_t* sp = slot_perm(k);
     if (wave * 16 < nq) {
       switch ((nk + 15) >> 4) {
-        case 1: pc_tile<D, T, GIVEN_LSE, HAS_E, 1, R>(p, buf, sp, qs, wave, pf, sq); break;
-        case 2: pc_tile<D, T, GIVEN_LSE, HAS_E, 2, R>(p, buf, sp, qs, wave, pf, sq); break;
-        case 3: pc_tile<D, T, GIVEN_LSE, HAS_E, 3, R>(p, buf, sp, qs, wave, pf, sq); break;
-        default: pc_tile<D, T, GIVEN_LSE, HAS_E, 4, R>(p, buf, sp, qs, wave, pf, sq); break;
+        case 1: pc_tile<D, T, GIVEN_LSE, HAS_E, 1, R>(p, buf, sp, qs, wave, pf, sq, gm); break;
+        case 2: pc_tile<D, T, GIVEN_LSE, HAS_E, 2, R>(p, buf, sp, qs, wave, pf, sq, gm); break;
+        case 3: pc_tile<D, T, GIVEN_LSE, HAS_E, 3, R>(p, buf, sp, qs, wave, pf, sq, gm); break;
+        default: pc_tile<D, T, GIVEN_LSE, HAS_E, 4, R>(p, buf, sp, qs, wave, pf, sq, gm); break;
       }
     } else {
       pf();
@@ -824,10 +824,10 @@ __device__ __forceinline__ void pc_consumer(const FwdParams& p, const char* lds,
       QSet<D, T> q3;
       pc_load_q<D, T, GIVEN_LSE>(p, q3, qs.b, qs.h, qs.n_phys, sp, 3);
       switch ((nk + 15) >> 4) {
-        case 1: pc_tile<D, T, GIVEN_LSE, HAS_E, 1, R>(p, buf, sp, q3, 3, [] {}, [] {}); break;
-        case 2: pc_tile<D, T, GIVEN_LSE, HAS_E, 2, R>(p, buf, sp, q3, 3, [] {}, [] {}); break;
-        case 3: pc_tile<D, T, GIVEN_LSE, HAS_E, 3, R>(p, buf, sp, q3, 3, [] {}, [] {}); break;
-        default: pc_tile<D, T, GIVEN_LSE, HAS_E, 4, R>(p, buf, sp, q3, 3, [] {}, [] {}); break;
+        case 1: pc_tile<D, T, GIVEN_LSE, HAS_E, 1, R>(p, buf, sp, q3, 3, [] {}, [] {}, gx); break;
+        case 2: pc_tile<D, T, GIVEN_LSE, HAS_E, 2, R>(p, buf, sp, q3, 3, [] {}, [] {}, gx); break;
+        case 3: pc_tile<D, T, GIVEN_LSE, HAS_E, 3, R>(p, buf, sp, q3, 3, [] {}, [] {}, gx); break;
+        default: pc_tile<D, T, GIVEN_LSE, HAS_E, 4, R>(p, buf, sp, q3, 3, [] {}, [] {}, gx); break;
       }
     }
     __builtin_amdgcn_s_waitcnt(kWaitLgkm0);

@@ -38,6 +38,19 @@ def fwd_jvp(q, k, v, mask, qt, kt, vt):
     return torch.func.jvp(lambda a, b, c: attention(a, b, c, mask), (q, k, v), (qt, kt, vt))
 
 
+def gated(q, k, v, mask):
+    """y [B,N,H/2,D]: :func:`attention` followed by the trunk's sigmoid-gate head collapse
+    (trunk.py:134-137), head h < H/2 gating head h + H/2."""
+    out = attention(q, k, v, mask)
+    hh = out.shape[2] // 2
+    return torch.sigmoid(out[:, :, :hh]) * out[:, :, hh:]
+
+
+def fwd_jvp_gated(q, k, v, mask, qt, kt, vt):
+    """(y, ydot) by forward-mode autodiff of :func:`gated`."""
+    return torch.func.jvp(lambda a, b, c: gated(a, b, c, mask), (q, k, v), (qt, kt, vt))
+
+
 def fwd_vjp(q, k, v, mask, dout):
     """(out, (dq, dk, dv)) by reverse-mode autodiff of :func:`attention`."""
     out, pullback = torch.func.vjp(lambda a, b, c: attention(a, b, c, mask), q, k, v)
@@ -58,7 +71,8 @@ def host_cpu_model() -> str:
 def time_walkers_per_s(work: str, B: int, N: int, H: int, D: int, n_phys: int, seed: int,
                        T: int = 1, bf16_inputs: bool = False, budget_s: float = 15.0,
                        threads: int | None = None) -> dict:
-    """Time ``work`` ('fwd', 'fwd_jvp' or 'fwd_vjp') on B walkers; returns walkers/s.
+    """Time ``work`` ('fwd', 'fwd_jvp', 'fwd_jvp_gated' or 'fwd_vjp') on B walkers; returns
+    walkers/s.
 
     Inputs follow the measurement recipe of the bench (default_rng(seed), N(0,1)/sqrt(D)
     for q/k/v, N(0,1) tangents and cotangent, the first n_phys sites physical). bf16
@@ -81,6 +95,9 @@ def time_walkers_per_s(work: str, B: int, N: int, H: int, D: int, n_phys: int, s
     elif work == "fwd_jvp":
         tans = [(draw(1.0), draw(1.0), draw(1.0)) for _ in range(T)]
         fn = lambda: [fwd_jvp(q, k, v, mask, *t) for t in tans]  # noqa: E731
+    elif work == "fwd_jvp_gated":
+        tans = [(draw(1.0), draw(1.0), draw(1.0)) for _ in range(T)]
+        fn = lambda: [fwd_jvp_gated(q, k, v, mask, *t) for t in tans]  # noqa: E731
     elif work == "fwd_vjp":
         dout = draw(1.0)
         fn = lambda: fwd_vjp(q, k, v, mask, dout)  # noqa: E731
