@@ -3,7 +3,8 @@
 The fused kernel's y = sigmoid(gate) * value and its tangents are compared with
 ``oracle.mhsea_oracle.gated_fwd_jvp`` (pinned in tests/test_gated_oracle.py) on seeded
 inputs, over T in {0, 1, 2}, D in {8, 16, 32}, prefix / scattered / empty masks, the key-mask
-mode, bias in both layouts, and grids where one workgroup walks several head pairs; and
+mode, bias in both layouts, the kernel's own two-direction variant (D <= 16) and the two-pass
+route (D = 32), and grids where one workgroup walks several head pairs; and
 against the unfused composition (hz_mhsea_fwd_jvp, then the collapse in torch) at c2's shape.
 Tolerance: max-norm relative error <= 1e-5 (float32).
 """
@@ -54,6 +55,9 @@ CASES = [
     (6, 300, 64, 8, 32, 1, "scattered", False, False, "qhk"),
     (7, 3, 8, 4, 16, 1, "prefix", False, True, "qhk"),
     (8, 11, 64, 4, 32, 0, "counts", True, False, "qhk"),
+    (9, 40, 64, 4, 16, 2, "scattered", False, True, "qkh"),
+    (10, 13, 33, 2, 8, 2, "counts", False, False, "qhk"),
+    (11, 25, 64, 8, 8, 1, "prefix", True, True, "qhk"),
 ]
 
 
