@@ -58,6 +58,8 @@ CASES = [
     (9, 40, 64, 4, 16, 2, "scattered", False, True, "qkh"),
     (10, 13, 33, 2, 8, 2, "counts", False, False, "qhk"),
     (11, 25, 64, 8, 8, 1, "prefix", True, True, "qhk"),
+    # the trunk's own call: n_heads 16 doubled for the gate, d_head 256 / 16 (config.py:20,26)
+    (12, 48, 64, 32, 16, 2, "prefix", False, True, "qkh"),
 ]
 
 
