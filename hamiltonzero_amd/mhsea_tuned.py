@@ -129,6 +129,55 @@ class _MhseaAD(torch.autograd.Function):
         return tout, None
 
 
+class _GatedAD(torch.autograd.Function):
+    """y = sigmoid(out[:, :, :H/2]) * out[:, :, H/2:] of MHSEA(q, k, e, v, mask), the trunk's
+    head collapse (trunk.py:134-137). The forward and forward mode run the fused kernel
+    (``hz_mhsea_fwd_jvp_gated``); reverse mode recomputes (out, lse), forms the collapse's
+    cotangent per head and runs the attention backward on it."""
+
+    @staticmethod
+    def forward(q, k, e, v, mask, opts):
+        scale, key_mask, e_layout = opts
+        y, _ = kernels.mhsea_fwd_jvp_gated(q, k, v, mask, e=e, scale=scale, key_mask=key_mask, e_layout=e_layout)
+        return y
+
+    @staticmethod
+    def setup_context(ctx, inputs, output):
+        q, k, e, v, mask, opts = inputs
+        ctx.opts = opts
+        ctx.save_for_backward(q, k, e, v, mask)
+        ctx.save_for_forward(q, k, e, v, mask)
+
+    @staticmethod
+    def backward(ctx, dy):
+        q, k, e, v, mask = ctx.saved_tensors
+        scale, key_mask, e_layout = ctx.opts
+        out, lse = kernels.mhsea_fwd(q, k, v, mask, e, scale=scale, key_mask=key_mask, e_layout=e_layout)
+        hh = out.shape[2] // 2
+        s = torch.sigmoid(out[:, :, :hh])
+        dout = torch.cat([dy * out[:, :, hh:] * s * (1 - s), dy * s], dim=2)
+        dq, dk, de, dv = kernels.mhsea_bwd(
+            q, k, v, mask, lse, out, dout, e,
+            want_de=bool(ctx.needs_input_grad[2]), scale=scale, key_mask=key_mask, e_layout=e_layout,
+        )
+        return dq, dk, de, dv, None, None
+
+    @staticmethod
+    def jvp(ctx, qt, kt, et, vt, _mask_t, _opts_t):
+        q, k, e, v, mask = ctx.saved_tensors
+        scale, key_mask, e_layout = ctx.opts
+        y, ty = kernels.mhsea_fwd_jvp_gated(q, k, v, mask, qt, kt, vt, e=e, et=et, scale=scale, key_mask=key_mask,
+                                            e_layout=e_layout)
+        return torch.zeros_like(y) if ty is None else ty
+
+
+def gated_edge_attention(q, k, e, v, mask, *, scale: float = 1.0, key_mask: bool = False, e_layout: str = "qhk"):
+    """Differentiable head-collapsed attention ``sigmoid(gate) * value`` (trunk.py:130-137 for
+    the tuned path): ``[B, N, H, D]`` operands with H = 2 * n_heads, result ``[B, N, H/2, D]``.
+    Serves what ``hz_mhsea_fwd_jvp_gated`` serves (fp32, N <= 64, D in {8, 16, 32})."""
+    return _GatedAD.apply(q, k, e, v, mask, (float(scale), bool(key_mask), e_layout))
+
+
 def mhsea_ad(q, k, e, v, mask, *, scale: float = 1.0, key_mask: bool = False, e_layout: str = "qhk"):
     """Differentiable (out, lse) with explicit scale / mask mode / bias layout."""
     return _MhseaAD.apply(q, k, e, v, mask, (float(scale), bool(key_mask), e_layout))

@@ -111,3 +111,42 @@ def test_gated_equals_unfused_composition_at_c2_shape():
     torch.cuda.synchronize()
     assert rel(y.cpu().numpy(), want_y.cpu().numpy()) <= TOL
     assert rel(ty.cpu().numpy(), want_ty.cpu().numpy()) <= TOL
+
+
+@pytest.mark.parametrize("with_e", [False, True])
+def test_gated_edge_attention_autograd(with_e):
+    """``gated_edge_attention``: reverse mode (recomputed out, lse; attention backward on the
+    collapse's cotangent) against the float64 oracle's VJP of the composite, and forward mode
+    (the fused kernel's tangent) against ``gated_fwd_jvp``."""
+    import torch.autograd.forward_ad as fwAD
+
+    from hamiltonzero_amd import gated_edge_attention
+
+    _say(f"gated autograd e={with_e}")
+    B, N, H, D = 3, 64, 4, 16
+    q, k, v, e, mask, tq, tk, tv, te = make(21, B, N, H, D, 1, "scattered", with_e, "qhk")
+    rng = np.random.default_rng(22)
+    dy = rng.standard_normal((B, N, H // 2, D), dtype=np.float32)
+    dev = lambda x, g=False: None if x is None else torch.from_numpy(x).cuda().requires_grad_(g)  # noqa: E731
+    scale = D ** -0.5
+    qd, kd, ed, vd = dev(q, True), dev(k, True), dev(e, with_e), dev(v, True)
+    y = gated_edge_attention(qd, kd, ed, vd, dev(mask), scale=scale)
+    y.backward(dev(dy))
+    torch.cuda.synchronize()
+    out, _ = O.fwd(q, k, e, v, mask, scale=scale)
+    s = 1.0 / (1.0 + np.exp(-out[:, :, : H // 2]))
+    dout = np.concatenate([dy * out[:, :, H // 2:] * s * (1 - s), dy * s], axis=2)
+    want = O.vjp(q, k, e, v, mask, dout, scale=scale)
+    assert rel(y.detach().cpu().numpy(), O.gate_collapse(out)) <= TOL
+    for name, got, ref in (("dq", qd.grad, want[0]), ("dk", kd.grad, want[1]), ("dv", vd.grad, want[3])):
+        assert rel(got.cpu().numpy(), ref) <= TOL, name
+    if with_e:
+        assert rel(ed.grad.cpu().numpy(), want[2]) <= TOL, "de"
+    with fwAD.dual_level():
+        duals = [fwAD.make_dual(dev(x), dev(t[0])) for x, t in ((q, tq), (k, tk), (v, tv))]
+        ee = fwAD.make_dual(dev(e), dev(te[0])) if with_e else None
+        yd = gated_edge_attention(duals[0], duals[1], ee, duals[2], dev(mask), scale=scale)
+        _, ty = fwAD.unpack_dual(yd)
+        torch.cuda.synchronize()
+        _, want_t = O.gated_fwd_jvp(q, k, e, v, mask, tq[0], tk[0], te[0] if with_e else None, tv[0], scale=scale)
+        assert rel(ty.cpu().numpy(), want_t) <= TOL
