@@ -132,6 +132,24 @@ int run_tangent_groups(hz::FwdParams p, int64_t D, int64_t T, bool given_lse, in
   return ok();
 }
 
+// Tangent operands of all T directions (the bases; the groups above shift them).
+void set_tangents(hz::FwdParams& p, void* tout, const void* qt, const void* kt, const void* et,
+                  const void* vt) {
+  p.tout = tout;
+  p.qt = qt;
+  p.kt = kt;
+  p.et = et;
+  p.vt = vt;
+}
+
+// Key-mask calls: rewrite the walkers without a physical site (the reference's float32
+// penalty, include/hz_mhsea.h); a no-op launch-free return in the square-mask mode.
+int keymask_empty_fwd(const hz::FwdParams& p, int64_t D, int64_t T, bool given_lse, int dtype,
+                      hipStream_t stream) {
+  if (!p.key_mask) return ok();
+  return launched(hz::launch_keymask_empty_fwd(p, static_cast<int>(D), static_cast<int>(T), given_lse, dtype, stream));
+}
+
 }  // namespace
 
 extern "C" {
@@ -155,7 +173,8 @@ int hz_mhsea_fwd(hipStream_t stream, const void* q, const void* k, const void* e
   hz::FwdParams p = fwd_params(q, k, e, v, mask, B, N, H, D, scale, flags);
   p.out = out;
   p.lse = lse;
-  return launched(hz::launch_fwd(p, static_cast<int>(D), 0, false, dtype, stream));
+  if (int rc = launched(hz::launch_fwd(p, static_cast<int>(D), 0, false, dtype, stream))) return rc;
+  return keymask_empty_fwd(p, D, 0, false, dtype, stream);
 }
 
 int hz_mhsea_jvp(hipStream_t stream, const void* q, const void* k, const void* e,
@@ -181,7 +200,9 @@ int hz_mhsea_jvp(hipStream_t stream, const void* q, const void* k, const void* e
   hz::FwdParams p = fwd_params(q, k, e, v, mask, B, N, H, D, scale, flags);
   p.out_in = out;
   p.lse_in = lse;
-  return run_tangent_groups(p, D, T, true, dtype, stream, tout, qt, kt, et, vt);
+  if (int rc = run_tangent_groups(p, D, T, true, dtype, stream, tout, qt, kt, et, vt)) return rc;
+  set_tangents(p, tout, qt, kt, et, vt);
+  return keymask_empty_fwd(p, D, T, true, dtype, stream);
 }
 
 int hz_mhsea_fwd_jvp(hipStream_t stream, const void* q, const void* k, const void* e,
@@ -207,7 +228,9 @@ int hz_mhsea_fwd_jvp(hipStream_t stream, const void* q, const void* k, const voi
   hz::FwdParams p = fwd_params(q, k, e, v, mask, B, N, H, D, scale, flags);
   p.out = out;
   p.lse = lse;
-  return run_tangent_groups(p, D, T, false, dtype, stream, tout, qt, kt, et, vt);
+  if (int rc = run_tangent_groups(p, D, T, false, dtype, stream, tout, qt, kt, et, vt)) return rc;
+  set_tangents(p, tout, qt, kt, et, vt);
+  return keymask_empty_fwd(p, D, T, false, dtype, stream);
 }
 
 int hz_mhsea_fwd_jvp_gated(hipStream_t stream, const void* q, const void* k, const void* e,
@@ -243,7 +266,10 @@ int hz_mhsea_fwd_jvp_gated(hipStream_t stream, const void* q, const void* k, con
   p.lse = nullptr;
   p.gated = 1;
   p.y_tstride = B * N * (H / 2) * D;
-  if (T == 0) return launched(hz::launch_fwd_pc(p, static_cast<int>(D), 0, false, stream));
+  if (T == 0) {
+    if (int rc = launched(hz::launch_fwd_pc(p, static_cast<int>(D), 0, false, stream))) return rc;
+    return keymask_empty_fwd(p, D, 0, false, HZ_DTYPE_F32, stream);
+  }
   // Later passes rewrite identical y values, so the call needs no scratch memory.
   const int64_t ts = p.t_stride, es = p.et_stride;
   auto shift = [](const void* base, int64_t off) -> const void* {
@@ -259,7 +285,8 @@ int hz_mhsea_fwd_jvp_gated(hipStream_t stream, const void* q, const void* k, con
     hipError_t err = hz::launch_fwd_pc(p, static_cast<int>(D), static_cast<int>(tn), false, stream);
     if (err != hipSuccess) return launched(err);
   }
-  return ok();
+  set_tangents(p, ty, qt, kt, et, vt);
+  return keymask_empty_fwd(p, D, T, false, HZ_DTYPE_F32, stream);
 }
 
 int hz_mhsea_bwd(hipStream_t stream, const void* q, const void* k, const void* e,
@@ -300,7 +327,9 @@ int hz_mhsea_bwd(hipStream_t stream, const void* q, const void* k, const void* e
   p.scale = scale;
   p.key_mask = (flags & HZ_FLAG_KEY_MASK) ? 1 : 0;
   p.force_generic = (flags & HZ_FLAG_GENERIC) ? 1 : 0;
-  return launched(hz::launch_bwd(p, static_cast<int>(D), dtype, stream));
+  if (int rc = launched(hz::launch_bwd(p, static_cast<int>(D), dtype, stream))) return rc;
+  if (!p.key_mask) return ok();
+  return launched(hz::launch_keymask_empty_bwd(p, static_cast<int>(D), dtype, stream));
 }
 
 int hz_rect_attention_fwd(hipStream_t stream, const float* q, const float* k, const float* v,

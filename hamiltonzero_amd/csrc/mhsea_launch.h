@@ -97,6 +97,14 @@ hipError_t device_cu_count(int* cus);
 hipError_t launch_fwd_small(const FwdParams& p, int D, int T, bool given_lse, int dtype,
                             hipStream_t stream);
 
+// Walkers with no physical site under the additive key mask (mhsea_keymask_empty.hip):
+// rewrites their results with the reference's float32-rounded penalised logits. Launched
+// after the main kernels of every HZ_FLAG_KEY_MASK call; tangent pointers are the bases of
+// all T directions. With p.gated it writes the collapse y / ty (float32).
+hipError_t launch_keymask_empty_fwd(const FwdParams& p, int D, int T, bool given_lse, int dtype,
+                                    hipStream_t stream);
+hipError_t launch_keymask_empty_bwd(const BwdParams& p, int D, int dtype, hipStream_t stream);
+
 // Rectangular attention with a dense [B, Nq, Nk, H] bias (rect_attention.hip).
 struct RectParams {
   const float* q;      // [B, Nq, H, D]

@@ -71,11 +71,20 @@ def _check_primals(q: Tensor, k: Tensor, v: Tensor, mask: Tensor, e: Optional[Te
             raise ValueError(f"e.shape must be {want}, got {tuple(e.shape)}")
         if e.dtype != q.dtype:
             raise TypeError(f"e.dtype must equal q.dtype ({q.dtype}), got {e.dtype}")
+        _on_device(q.device, e=e)
     return B, N, H, D
 
 
 def _c(t: Optional[Tensor]) -> Optional[Tensor]:
     return None if t is None else t.contiguous()
+
+
+def _on_device(device: torch.device, **tensors: Optional[Tensor]) -> None:
+    """Every given tensor operand must live on ``device`` (the GPU of q): the kernels receive
+    raw device pointers, so a host tensor here would be a memory fault, not an error."""
+    for name, t in tensors.items():
+        if t is not None and t.device != device:
+            raise ValueError(f"{name} is on {t.device}, q on {device}: every tensor operand must be on q's GPU")
 
 
 def _mask_u8(mask: Tensor, device: torch.device) -> Tensor:
@@ -104,6 +113,7 @@ def _tangents(q, e_shape, qt, kt, et, vt):
     kt, tk = _tangent(kt, shape, q.dtype, "kt")
     vt, tv = _tangent(vt, shape, q.dtype, "vt")
     et, te = _tangent(et, e_shape, q.dtype, "et")
+    _on_device(q.device, qt=qt, kt=kt, vt=vt, et=et)
     counts = {x for x in (tq, tk, tv, te) if x}
     if len(counts) > 1:
         raise ValueError(f"tangent directions disagree: {sorted(counts)}")
@@ -170,6 +180,7 @@ def mhsea_jvp(
         raise ValueError("out must match q in shape and dtype")
     if tuple(lse.shape) != (B, N, H) or lse.dtype != torch.float32:
         raise ValueError(f"lse must be float32 of shape {(B, N, H)}")
+    _on_device(q.device, out=out, lse=lse)
     q, k, v, e, out, lse = _c(q), _c(k), _c(v), _c(e), _c(out), _c(lse)
     m = _mask_u8(mask, q.device)
     tout = torch.empty((T, B, N, H, D), dtype=q.dtype, device=q.device)
@@ -289,6 +300,7 @@ def mhsea_bwd(
             raise ValueError(f"{name} must match q in shape and dtype")
     if tuple(lse.shape) != (B, N, H) or lse.dtype != torch.float32:
         raise ValueError(f"lse must be float32 of shape {(B, N, H)}")
+    _on_device(q.device, lse=lse, out=out, dout=dout)
     q, k, v, e, lse, out, dout = map(_c, (q, k, v, e, lse, out, dout))
     m = _mask_u8(mask, q.device)
     dq = torch.empty_like(q)
@@ -337,6 +349,7 @@ def rect_attention_fwd(
         raise ValueError(f"bias must have shape {(B, Nq, Nk, H)}, got {tuple(bias.shape)}")
     if key_mask is not None and tuple(key_mask.shape) != (B, Nk):
         raise ValueError(f"key_mask must have shape {(B, Nk)}, got {tuple(key_mask.shape)}")
+    _on_device(q.device, k=k, v=v, bias=bias)
     q, k, v, bias = map(_c, (q, k, v, bias))
     m = None if key_mask is None else _mask_u8(key_mask, q.device)
     out = torch.empty_like(q)

@@ -41,9 +41,17 @@
  *          pairs are -1e4 (utils.py:51-52). Rows of masked queries are written as exact
  *          zeros in out / tout / dq, and their lse is -1e4 + log(N).
  *      HZ_FLAG_KEY_MASK (reference_edge_attention, pallas_attention.py:34-36):
- *          only keys are masked (additive -1e9); every query row is computed. If no key
- *          of a walker is physical, all keys are used (the exact-arithmetic limit of the
- *          additive mask).
+ *          only keys are masked (additive -1e9); every query row is computed. The
+ *          reference adds the penalty in float32, so a masked key's logit is fl32(s - 1e9),
+ *          a multiple of 64. While a walker has a physical key, masked keys get weight
+ *          exactly 0 (and are never read). If NO key of a walker is physical, every key is
+ *          used with the logit fl32(fl32(s - 1e9) + 1e9) — the reference's rounded value
+ *          shifted back by the constant 1e9, which softmax ignores — so all |s| < 32 give
+ *          uniform weights (out = mean of the walker's value rows), as in the reference;
+ *          that walker's lse is relative to the shift. Tangents and cotangents use the
+ *          same weights (the penalty's derivative is 1, as under autodiff).
+ *          One intended difference on non-finite inputs: a NaN / Inf in a masked key's
+ *          k, v or bias reaches the reference's output (0 * NaN), not this library's.
  *  - Every call is enqueue-only on `stream` (no host synchronisation), allocates nothing,
  *    fully overwrites its outputs (including masked rows), and is deterministic
  *    (no atomics). Calls on distinct output buffers are re-entrant.

@@ -17,7 +17,14 @@ Two mask modes:
   the tangent are zero (``_pallas_attn/mhsea_tuned.py:91``,
   ``_pallas_attn/mhsea_tuned_jvp.py:88-91``).
 * ``key_mask=True`` — ``reference_edge_attention`` (``pallas_attention.py:22-37``): an
-  additive ``-1e9 * (1 - mask_k)`` on the logits, nothing zeroed.
+  additive ``-1e9 * (1 - mask_k)`` on the logits, nothing zeroed. The reference adds the
+  penalty in float32 (``:34-35``), so a masked key's logit is ``fl32(s - 1e9)``: a multiple
+  of 64 (the float32 spacing at 1e9). While one key is physical this only means that
+  masked keys get weight exactly 0; when no key of a walker is physical the softmax runs
+  over these rounded logits (uniform weights when every ``|s| < 32``). This oracle
+  evaluates that penalty in float32 and, for a walker with no physical key, reports its
+  scores and lse shifted back by the constant 1e9 (``fl32(s - 1e9) + 1e9``, exact), which
+  the softmax ignores.
 
 How each function is pinned (tests/test_oracle.py): the forward by explicit loops on
 tiny inputs and closed-form special cases; the tangent by central finite differences of
@@ -36,6 +43,23 @@ KEY_MASK_PENALTY = -1e9  # pallas_attention.py:34
 
 def _f64(x):
     return None if x is None else np.asarray(x, dtype=np.float64)
+
+
+def _es(spec, a, b):
+    """float64 einsum of two operands (contraction order chosen by numpy for speed)."""
+    return np.einsum(spec, a, b, optimize=True)
+
+
+def _penalised(s, mask):
+    """Logits of the additive key mask as the reference's float32 arithmetic forms them
+    (pallas_attention.py:34-35): physical keys keep ``s``; a masked key's logit is
+    ``fl32(fl32(s) - 1e9)``. For a walker with no physical key the result is shifted back by
+    the constant 1e9 (exact: the rounded values are integers), which softmax ignores."""
+    pen = (s.astype(np.float32) + np.float32(KEY_MASK_PENALTY)).astype(np.float64)
+    out = np.where(mask[:, None, None, :], s, pen)
+    empty = ~mask.any(axis=1)
+    out[empty] -= KEY_MASK_PENALTY
+    return out
 
 
 def _e_bhqk(e, e_layout):
@@ -83,11 +107,11 @@ def scores(q, k, e, mask, *, scale=1.0, key_mask=False, e_layout="qhk"):
     q, k = _f64(q), _f64(k)
     mask = np.asarray(mask, dtype=bool)
     if key_mask:
-        s = np.einsum("bihd,bjhd->bhij", q, k) * scale + _e_bhqk(e, e_layout)
-        return s + (1.0 - mask[:, None, None, :]) * KEY_MASK_PENALTY
+        s = _es("bihd,bjhd->bhij", q, k) * scale + _e_bhqk(e, e_layout)
+        return _penalised(s, mask)
     q = _zero_rows(q, mask)
     k = _zero_rows(k, mask)
-    s = np.einsum("bihd,bjhd->bhij", q * scale, k) + _e_bhqk(e, e_layout)
+    s = _es("bihd,bjhd->bhij", q * scale, k) + _e_bhqk(e, e_layout)
     return np.where(_valid(mask, False), s, MASK_SCORE)
 
 
@@ -97,16 +121,22 @@ def fwd(q, k, e, v, mask, *, scale=1.0, key_mask=False, e_layout="qhk"):
     lse = max + log(sum(exp(S - max))), P = exp(S - lse), out = P v (mhsea.py:26-31);
     masked rows of out zeroed (mhsea_tuned.py:91) unless ``key_mask``.
     """
+    out, lse, _ = _forward(q, k, e, v, mask, scale, key_mask, e_layout)
+    return out, lse
+
+
+def _forward(q, k, e, v, mask, scale, key_mask, e_layout):
+    """(out, lse, P) of ``fwd``, P [B, H, Nq, Nk] the softmax weights."""
     mask = np.asarray(mask, dtype=bool)
     s = scores(q, k, e, mask, scale=scale, key_mask=key_mask, e_layout=e_layout)
     m = s.max(axis=-1, keepdims=True)
     lse = m + np.log(np.exp(s - m).sum(axis=-1, keepdims=True))
     p = np.exp(s - lse)
     v = _f64(v) if key_mask else _zero_rows(_f64(v), mask)
-    out = np.einsum("bhij,bjhd->bihd", p, v)
+    out = _es("bhij,bjhd->bihd", p, v)
     if not key_mask:
         out = _zero_rows(out, mask)
-    return out, lse[..., 0].transpose(0, 2, 1)
+    return out, lse[..., 0].transpose(0, 2, 1), p
 
 
 def probs(q, k, e, mask, *, scale=1.0, key_mask=False, e_layout="qhk"):
@@ -129,19 +159,18 @@ def jvp(q, k, e, v, mask, qt, kt, et, vt, *, scale=1.0, key_mask=False, e_layout
     qt = z if qt is None else _f64(qt)
     kt = z if kt is None else _f64(kt)
     vt = z if vt is None else _f64(vt)
-    p = probs(q, k, e, mask, scale=scale, key_mask=key_mask, e_layout=e_layout)
-    out, _ = fwd(q, k, e, v, mask, scale=scale, key_mask=key_mask, e_layout=e_layout)
+    out, _, p = _forward(q, k, e, v, mask, scale, key_mask, e_layout)
     if not key_mask:
         q, k, v, qt, kt, vt = (_zero_rows(x, mask) for x in (q, k, v, qt, kt, vt))
-    ds = scale * (np.einsum("bihd,bjhd->bhij", qt, k) + np.einsum("bihd,bjhd->bhij", q, kt))
+    ds = scale * (_es("bihd,bjhd->bhij", qt, k) + _es("bihd,bjhd->bhij", q, kt))
     if et is not None:
         ds = ds + _e_bhqk(et, e_layout)
     ds = np.where(_valid(mask, key_mask), ds, 0.0)
     pds = p * ds
     mean = pds.sum(axis=-1)  # [B, H, Nq]
     tout = (
-        np.einsum("bhij,bjhd->bihd", pds, v)
-        + np.einsum("bhij,bjhd->bihd", p, vt)
+        _es("bhij,bjhd->bihd", pds, v)
+        + _es("bhij,bjhd->bihd", p, vt)
         - mean.transpose(0, 2, 1)[..., None] * out
     )
     if not key_mask:
@@ -158,16 +187,15 @@ def vjp(q, k, e, v, mask, dout, *, scale=1.0, key_mask=False, e_layout="qhk"):
     """
     mask = np.asarray(mask, dtype=bool)
     q, k, v, dout = _f64(q), _f64(k), _f64(v), _f64(dout)
-    p = probs(q, k, e, mask, scale=scale, key_mask=key_mask, e_layout=e_layout)
-    out, _ = fwd(q, k, e, v, mask, scale=scale, key_mask=key_mask, e_layout=e_layout)
+    out, _, p = _forward(q, k, e, v, mask, scale, key_mask, e_layout)
     if not key_mask:
         q, k, v, dout = (_zero_rows(x, mask) for x in (q, k, v, dout))
-    dp = np.einsum("bihd,bjhd->bhij", dout, v)
+    dp = _es("bihd,bjhd->bhij", dout, v)
     delta = (out * dout).sum(axis=-1).transpose(0, 2, 1)[..., None]  # [B, H, Nq, 1]
     ds = (dp - delta) * p * _valid(mask, key_mask)
-    dq = scale * np.einsum("bhij,bjhd->bihd", ds, k)
-    dk = scale * np.einsum("bhij,bihd->bjhd", ds, q)
-    dv = np.einsum("bhij,bihd->bjhd", p, dout)
+    dq = scale * _es("bhij,bjhd->bihd", ds, k)
+    dk = scale * _es("bhij,bihd->bjhd", ds, q)
+    dv = _es("bhij,bihd->bjhd", p, dout)
     if not key_mask:
         dv = _zero_rows(dv, mask)
     return dq, dk, _e_back(ds, e_layout), dv
@@ -233,8 +261,12 @@ def loop_fwd(q, k, e, v, mask, *, scale=1.0, key_mask=False, e_layout="qhk"):
                     bias = 0.0
                     if e is not None:
                         bias = e[b, i, h, j] if e_layout == "qhk" else e[b, i, j, h]
-                    if key_mask:
-                        sij = dot + bias + (0.0 if mask[b, j] else KEY_MASK_PENALTY)
+                    if key_mask and mask[b, j]:
+                        sij = dot + bias
+                    elif key_mask:  # float32 penalty; shifted back by 1e9 if no key is physical
+                        sij = float(np.float32(np.float32(dot + bias) + np.float32(KEY_MASK_PENALTY)))
+                        if not mask[b].any():
+                            sij -= KEY_MASK_PENALTY
                     else:
                         sij = dot + bias if (mask[b, i] and mask[b, j]) else MASK_SCORE
                     row.append(sij)

@@ -137,6 +137,74 @@ def test_reference_edge_attention_matches_formula():
     assert rel(O.reference_edge_attention(Q, K, V, E, mask), want) < 1e-13
 
 
+def _fp32_literal_edge_attention(Q, K, V, E, mask):
+    """pallas_attention.py:30-37 evaluated literally in numpy float32, one operation at a
+    time: einsum, * d^-1/2, + e^T, + (1 - mask) * -1e9, softmax as exp(x - max) / sum."""
+    Q, K, V, E = (np.asarray(x, dtype=np.float32) for x in (Q, K, V, E))
+    sm_scale = np.float32(float(Q.shape[-1]) ** -0.5)
+    logits = np.einsum("ihd,jhd->hij", Q, K) * sm_scale
+    logits = logits + np.transpose(E, (2, 0, 1))
+    logits = logits + (np.float32(1.0) - mask.astype(np.float32))[None, None, :] * np.float32(-1e9)
+    assert logits.dtype == np.float32
+    ex = np.exp(logits - logits.max(-1, keepdims=True))
+    alpha = ex / ex.sum(-1, keepdims=True)
+    return np.einsum("hij,jhd->ihd", alpha, V)
+
+
+def _exact_limit(Q, K, V, E):
+    """softmax(s) V over every key: the exact-arithmetic limit of the additive mask when no
+    key is physical (what the reference's float32 arithmetic does NOT compute)."""
+    logits = np.einsum("ihd,jhd->hij", Q, K) / np.sqrt(Q.shape[-1]) + E.transpose(2, 0, 1)
+    a = np.exp(logits - logits.max(-1, keepdims=True))
+    return np.einsum("hij,jhd->ihd", a / a.sum(-1, keepdims=True), V)
+
+
+def test_key_mask_matches_float32_literal_partially_masked():
+    rng = np.random.default_rng(21)
+    n, h, d = 9, 2, 16
+    Q, K, V = (rng.standard_normal((n, h, d)).astype(np.float32) for _ in range(3))
+    E = rng.standard_normal((n, n, h)).astype(np.float32)
+    mask = np.array([1, 0, 1, 1, 0, 0, 1, 0, 1], dtype=bool)
+    assert rel(O.reference_edge_attention(Q, K, V, E, mask), _fp32_literal_edge_attention(Q, K, V, E, mask)) < 1e-5
+
+
+def test_key_mask_all_masked_small_logits_is_uniform():
+    """No physical key, every |logit| < 32: fl32(s - 1e9) = -1e9 for every key, so the
+    reference averages all value rows; the exact-arithmetic limit does not."""
+    rng = np.random.default_rng(22)
+    n, h, d = 8, 3, 32
+    Q, K, V = (rng.standard_normal((n, h, d)).astype(np.float32) for _ in range(3))
+    E = rng.standard_normal((n, n, h)).astype(np.float32)
+    mask = np.zeros(n, dtype=bool)
+    lit = _fp32_literal_edge_attention(Q, K, V, E, mask)
+    mean_v = np.broadcast_to(V.astype(np.float64).mean(axis=0), (n, h, d))
+    assert rel(lit, mean_v) < 1e-6
+    got = O.reference_edge_attention(Q, K, V, E, mask)
+    assert rel(got, lit) < 1e-6
+    assert rel(_exact_limit(Q, K, V, E), lit) > 1e-2  # the test tells the two apart
+    _, lse = O.fwd(Q[None], K[None], E[None], V[None], mask[None], scale=d ** -0.5, key_mask=True,
+                   e_layout="qkh")
+    np.testing.assert_allclose(lse, np.log(n), rtol=0, atol=1e-12)  # shifted logits all 0
+
+
+def test_key_mask_all_masked_large_logits_rounds_to_multiples_of_64():
+    """No physical key, logits of a few hundred: fl32(s - 1e9) keeps s to the nearest
+    multiple of 64, so the weights concentrate on the keys of the top multiple."""
+    rng = np.random.default_rng(23)
+    n, h, d = 12, 2, 16
+    Q, K, V = (rng.standard_normal((n, h, d)).astype(np.float32) for _ in range(3))
+    Q *= np.float32(12.0)
+    K *= np.float32(12.0)
+    E = (rng.standard_normal((n, n, h)) * 40.0).astype(np.float32)
+    s = np.einsum("ihd,jhd->hij", Q.astype(np.float64), K) / np.sqrt(d) + E.transpose(2, 0, 1)
+    assert np.abs(s).max() > 200.0
+    assert np.min(np.abs((s - 32.0) / 64.0 - np.round((s - 32.0) / 64.0))) * 64.0 > 0.05  # no tie
+    mask = np.zeros(n, dtype=bool)
+    lit = _fp32_literal_edge_attention(Q, K, V, E, mask)
+    assert rel(O.reference_edge_attention(Q, K, V, E, mask), lit) < 1e-5
+    assert rel(_exact_limit(Q, K, V, E), lit) > 1e-2
+
+
 # ----------------------------------------------------------------------------- tangent
 def _tangents(rng, q, e):
     return (
