@@ -9,6 +9,10 @@ primitive's square mask and zeroed masked rows, ``_pallas_attn/mhsea.py:18-25``,
 ``_pallas_attn/mhsea_tuned.py:91``). Forward-mode uses ``torch.func.jvp`` (as JAX's jvp
 of the jnp path would), reverse mode ``torch.func.vjp``. The reference's own files are
 not executed (JAX is not installed).
+
+``time_walkers_per_s`` runs on the bench's own inputs (a walker sample of the GPU batch)
+and returns the outputs of its last repetition, so the bench can compare them with the
+GPU's results for the same walkers.
 """
 
 from __future__ import annotations
@@ -16,12 +20,11 @@ from __future__ import annotations
 import os
 import time
 
-import numpy as np
 import torch
 
 
 def attention(q, k, v, mask, e=None):
-    """out [B,N,H,D] of the primitive semantics, float32, on CPU tensors."""
+    """out [B,N,H,D] of the primitive semantics, float32, on CPU tensors; e [B,N,H,N]."""
     valid = mask[:, None, :, None] & mask[:, None, None, :]
     mq = mask[:, :, None, None].to(q.dtype)
     s = torch.einsum("bihd,bjhd->bhij", q * mq, k * mq)
@@ -33,27 +36,31 @@ def attention(q, k, v, mask, e=None):
     return out * mq
 
 
-def fwd_jvp(q, k, v, mask, qt, kt, vt):
+def fwd_jvp(q, k, v, mask, qt, kt, vt, e=None, et=None):
     """(out, tout) by forward-mode autodiff of :func:`attention`."""
-    return torch.func.jvp(lambda a, b, c: attention(a, b, c, mask), (q, k, v), (qt, kt, vt))
+    if e is None:
+        return torch.func.jvp(lambda a, b, c: attention(a, b, c, mask), (q, k, v), (qt, kt, vt))
+    return torch.func.jvp(lambda a, b, c, d: attention(a, b, c, mask, d), (q, k, v, e), (qt, kt, vt, et))
 
 
-def gated(q, k, v, mask):
+def gated(q, k, v, mask, e=None):
     """y [B,N,H/2,D]: :func:`attention` followed by the trunk's sigmoid-gate head collapse
     (trunk.py:134-137), head h < H/2 gating head h + H/2."""
-    out = attention(q, k, v, mask)
+    out = attention(q, k, v, mask, e)
     hh = out.shape[2] // 2
     return torch.sigmoid(out[:, :, :hh]) * out[:, :, hh:]
 
 
-def fwd_jvp_gated(q, k, v, mask, qt, kt, vt):
+def fwd_jvp_gated(q, k, v, mask, qt, kt, vt, e=None, et=None):
     """(y, ydot) by forward-mode autodiff of :func:`gated`."""
-    return torch.func.jvp(lambda a, b, c: gated(a, b, c, mask), (q, k, v), (qt, kt, vt))
+    if e is None:
+        return torch.func.jvp(lambda a, b, c: gated(a, b, c, mask), (q, k, v), (qt, kt, vt))
+    return torch.func.jvp(lambda a, b, c, d: gated(a, b, c, mask, d), (q, k, v, e), (qt, kt, vt, et))
 
 
-def fwd_vjp(q, k, v, mask, dout):
+def fwd_vjp(q, k, v, mask, dout, e=None):
     """(out, (dq, dk, dv)) by reverse-mode autodiff of :func:`attention`."""
-    out, pullback = torch.func.vjp(lambda a, b, c: attention(a, b, c, mask), q, k, v)
+    out, pullback = torch.func.vjp(lambda a, b, c: attention(a, b, c, mask, e), q, k, v)
     return out, pullback(dout)
 
 
@@ -68,46 +75,63 @@ def host_cpu_model() -> str:
     return "unknown"
 
 
-def time_walkers_per_s(work: str, B: int, N: int, H: int, D: int, n_phys: int, seed: int,
-                       T: int = 1, bf16_inputs: bool = False, budget_s: float = 15.0,
-                       threads: int | None = None) -> dict:
-    """Time ``work`` ('fwd', 'fwd_jvp', 'fwd_jvp_gated' or 'fwd_vjp') on B walkers; returns
-    walkers/s.
+def host_cpus() -> dict:
+    """What the host offers this process: os.cpu_count(), the CPUs of its affinity mask and
+    the cgroup CPU quota (cpu.max), if any."""
+    info = {"os_cpu_count": os.cpu_count(), "affinity_cpus": len(os.sched_getaffinity(0)), "cgroup_cpu_quota": None}
+    try:
+        with open("/sys/fs/cgroup/cpu.max") as fh:
+            quota, period = fh.read().split()[:2]
+            if quota != "max":
+                info["cgroup_cpu_quota"] = int(quota) / int(period)
+    except (OSError, ValueError):
+        pass
+    return info
 
-    Inputs follow the measurement recipe of the bench (default_rng(seed), N(0,1)/sqrt(D)
-    for q/k/v, N(0,1) tangents and cotangent, the first n_phys sites physical). bf16
-    configurations run in float32 on bf16-rounded inputs.
-    """
-    threads = threads or os.cpu_count() or 1
+
+def default_threads() -> int:
+    """Every host core this process may use: the affinity mask, capped by a cgroup quota."""
+    info = host_cpus()
+    n = info["affinity_cpus"] or info["os_cpu_count"] or 1
+    if info["cgroup_cpu_quota"]:
+        n = min(n, max(1, int(info["cgroup_cpu_quota"])))
+    return n
+
+
+def time_walkers_per_s(work: str, inputs: dict, budget_s: float = 15.0, threads: int | None = None) -> dict:
+    """Time ``work`` ('fwd', 'fwd_jvp', 'fwd_jvp_gated' or 'fwd_vjp') on the walkers of
+    ``inputs`` (CPU float32 tensors: q, k, v, mask, optional e; tangents qt, kt, vt, et as
+    [T, ...] for the forward-mode works; dout for 'fwd_vjp'). Returns walkers/s and the
+    outputs of the last repetition ('out', 'tout' [T, ...], 'y', 'ty', 'dq', 'dk', 'dv')."""
+    threads = threads or default_threads()
     torch.set_num_threads(threads)
-    rng = np.random.default_rng(seed)
-    shape = (B, N, H, D)
+    q, k, v, mask, e = (inputs.get(n) for n in ("q", "k", "v", "mask", "e"))
+    B = q.shape[0]
+    if work in ("fwd_jvp", "fwd_jvp_gated"):
+        T = inputs["qt"].shape[0]
+        et = inputs.get("et")
+        f = fwd_jvp if work == "fwd_jvp" else fwd_jvp_gated
 
-    def draw(scale):
-        x = torch.from_numpy(rng.standard_normal(shape, dtype=np.float32) * np.float32(scale))
-        return x.to(torch.bfloat16).float() if bf16_inputs else x
-
-    q, k, v = draw(D ** -0.5), draw(D ** -0.5), draw(D ** -0.5)
-    mask = torch.zeros((B, N), dtype=torch.bool)
-    mask[:, :n_phys] = True
-    if work == "fwd":
-        fn = lambda: attention(q, k, v, mask)  # noqa: E731
-    elif work == "fwd_jvp":
-        tans = [(draw(1.0), draw(1.0), draw(1.0)) for _ in range(T)]
-        fn = lambda: [fwd_jvp(q, k, v, mask, *t) for t in tans]  # noqa: E731
-    elif work == "fwd_jvp_gated":
-        tans = [(draw(1.0), draw(1.0), draw(1.0)) for _ in range(T)]
-        fn = lambda: [fwd_jvp_gated(q, k, v, mask, *t) for t in tans]  # noqa: E731
+        def fn():
+            res = [f(q, k, v, mask, inputs["qt"][t], inputs["kt"][t], inputs["vt"][t], e,
+                     None if et is None else et[t]) for t in range(T)]
+            prim = res[0][0]
+            tans = torch.stack([r[1] for r in res])
+            return {"out": prim, "tout": tans} if work == "fwd_jvp" else {"y": prim, "ty": tans}
+    elif work == "fwd":
+        def fn():
+            return {"out": attention(q, k, v, mask, e)}
     elif work == "fwd_vjp":
-        dout = draw(1.0)
-        fn = lambda: fwd_vjp(q, k, v, mask, dout)  # noqa: E731
+        def fn():
+            out, (dq, dk, dv) = fwd_vjp(q, k, v, mask, inputs["dout"], e)
+            return {"out": out, "dq": dq, "dk": dk, "dv": dv}
     else:
         raise ValueError(work)
     with torch.no_grad() if work == "fwd" else torch.enable_grad():
-        fn()  # warm-up
+        res = fn()  # warm-up
         reps, t0 = 0, time.perf_counter()
         while True:
-            fn()
+            res = fn()
             reps += 1
             el = time.perf_counter() - t0
             if el >= budget_s or reps >= 100000:
@@ -118,6 +142,8 @@ def time_walkers_per_s(work: str, B: int, N: int, H: int, D: int, n_phys: int, s
         "reps": reps,
         "threads": threads,
         "cpu_model": host_cpu_model(),
+        "host_cpus": host_cpus(),
+        "outputs": {n: t.detach() for n, t in res.items()},
     }
 
 
@@ -129,36 +155,28 @@ def rect_attention(q, k, v, bias, key_mask, scale):
     return torch.einsum("bhij,bjhd->bihd", torch.softmax(s, dim=-1), v)
 
 
-def time_rect_queries_per_s(Nq_sample: int, Nk: int, H: int, D: int, n_phys: int, seed: int,
-                            budget_s: float = 15.0, threads: int | None = None) -> dict:
-    """Time the rectangular forward for ``Nq_sample`` query rows of one system against all
-    ``Nk`` keys (a sequence-parallel rank's share); returns query rows per second."""
-    threads = threads or os.cpu_count() or 1
+def time_rect_queries_per_s(q, k, v, bias, key_mask, scale, budget_s: float = 15.0,
+                            threads: int | None = None) -> dict:
+    """Time the rectangular forward for the query rows of ``q [1, Nq_sample, H, D]`` against
+    all keys (a sequence-parallel rank's share); returns query rows per second and the
+    output of the last repetition."""
+    threads = threads or default_threads()
     torch.set_num_threads(threads)
-    rng = np.random.default_rng(seed)
-
-    def draw(shape, scale):
-        return torch.from_numpy(rng.standard_normal(shape, dtype=np.float32) * np.float32(scale))
-
-    q = draw((1, Nq_sample, H, D), 1.0)
-    k = draw((1, Nk, H, D), 1.0)
-    v = draw((1, Nk, H, D), 1.0)
-    bias = draw((1, Nq_sample, Nk, H), D ** -0.5)
-    mask = torch.zeros((1, Nk), dtype=torch.bool)
-    mask[:, :n_phys] = True
     with torch.no_grad():
-        rect_attention(q, k, v, bias, mask, D ** -0.5)  # warm-up
+        out = rect_attention(q, k, v, bias, key_mask, scale)  # warm-up
         reps, t0 = 0, time.perf_counter()
         while True:
-            rect_attention(q, k, v, bias, mask, D ** -0.5)
+            out = rect_attention(q, k, v, bias, key_mask, scale)
             reps += 1
             el = time.perf_counter() - t0
             if el >= budget_s or reps >= 100000:
                 break
     return {
-        "queries_per_s": Nq_sample * reps / el,
+        "queries_per_s": q.shape[1] * reps / el,
         "seconds": el,
         "reps": reps,
         "threads": threads,
         "cpu_model": host_cpu_model(),
+        "host_cpus": host_cpus(),
+        "out": out,
     }

@@ -1,0 +1,57 @@
+"""Host-side checks of bench.py: the algorithmic bytes / flops behind ``roofline`` equal the
+per-configuration figures of the measurement definition (every [B, L, H, D] tensor moved
+once, mask as uint8, (2 + 4T) G / 6G / 2G flops with G = 2 L^2 D per walker and head), and
+the multi-GPU request is refused with a message."""
+
+import subprocess
+import sys
+from pathlib import Path
+
+import pytest
+
+ROOT = Path(__file__).resolve().parents[1]
+sys.path.insert(0, str(ROOT))
+
+import bench  # noqa: E402
+
+
+@pytest.mark.parametrize(
+    "name,bytes_,flops",
+    [
+        ("c1", 4_196_352, 8_388_608),
+        ("c2", 536_936_448, 12_884_901_888),
+        ("c3", 3_238_264_832, 103_079_215_104),
+        ("c4", 2_147_614_720, 206_158_430_208),
+        ("c5", 3_221_356_544, 2_748_779_069_440),
+    ],
+)
+def test_padded_figures(name, bytes_, flops):
+    c = bench.CONFIGS[name]
+    a = bench.algorithmic(c.work, c.B, c.N, c.H, c.D, c.n_phys, c.T, 2 if c.dtype == "bf16" else 4, c.with_e)
+    assert a["padded_bytes"] == bytes_
+    assert a["padded_flops"] == flops
+
+
+def test_bias_adds_e_and_its_tangents():
+    c = bench.CONFIGS["c2e"]
+    plain = bench.algorithmic("fwd_jvp", c.B, c.N, c.H, c.D, c.n_phys, c.T, 4, False)
+    with_e = bench.algorithmic("fwd_jvp", c.B, c.N, c.H, c.D, c.n_phys, c.T, 4, True)
+    assert with_e["padded_bytes"] - plain["padded_bytes"] == 268_435_456  # e and et, fp32
+    assert with_e["eff_bytes"] - plain["eff_bytes"] == 2 * 1024 * 36 * 8 * 36 * 4
+
+
+def test_split_route_is_charged_the_fused_figure():
+    c = bench.CONFIGS["c2split"]
+    a = bench.algorithmic(c.work, c.B, c.N, c.H, c.D, c.n_phys, c.T, 4)
+    assert a["padded_bytes"] == 536_936_448
+
+
+def test_c4_runs_in_chunks_of_16():
+    assert bench.CONFIGS["c4"].chunk == 16 and bench.CONFIGS["c4"].B == 512
+
+
+def test_multi_gpu_request_is_refused():
+    r = subprocess.run([sys.executable, str(ROOT / "bench.py"), "--gpus", "2"], capture_output=True, text=True,
+                       timeout=120)
+    assert r.returncode == 2
+    assert "one GPU" in r.stderr
