@@ -12,7 +12,8 @@ those walkers are compared with the GPU's (``cpu_baseline.check``), outside the 
 Beside the hot path (never the default line): ``c2split`` (the reference's two-launch
 drop-in, forward then tangent from (out, lse)), ``c2e`` (c2 with the pair bias e and its
 tangent), ``gate`` / ``gate_trunk`` (the trunk's sigmoid-gate head collapse fused), ``rect``
-(the large-N rectangular forward).
+(the large-N rectangular forward), ``merge`` (one tree level of the compiled per-walker
+executor: quadrilinear merge + residual factorized apply).
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--config NAME]
                        [--cpu-budget SECONDS] [--no-cpu-baseline]
@@ -35,6 +36,7 @@ METRIC = "fwd+JVP attention walkers/sec at B=1024,L=64; % of MFMA/HBM roofline"
 GATE_METRIC = ("fwd+JVP attention with the sigmoid-gate head collapse fused, walkers/sec at B=1024,L=64; "
                "% of MFMA/HBM roofline")
 RECT_METRIC = "rectangular large-N forward (noncausal_bias_mha) query rows/sec; % of MFMA/HBM roofline"
+EXECUTOR_METRIC = "compiled-executor merge level (quadrilinear merge + factorized apply) walkers/sec; % of MFMA roofline"
 HBM_PEAK_GBS = 8000.0
 FP32_PEAK_TFLOPS = 157.3
 BF16_PEAK_TFLOPS = 2516.6
@@ -90,6 +92,13 @@ CONFIGS = {
                          "the trunk's attention call: [1024,64,32,16] with pair bias e [1024,64,32,64] and its "
                          "tangent, gate collapse fused -> y, ydot [1024,64,16,16], 36/64 physical sites",
                          with_e=True, metric=GATE_METRIC),
+    # One tree level of the compiled per-walker executor at the fine-tune ranks: the
+    # quadrilinear merge of node pairs and the residual factorized apply
+    # (compiled/execute.py:103-104; merge_dim 1536 = 48 groups of rank 32, merge_rank 1024).
+    "merge": Config("executor", 1024, 32, 48, 32, 1024, 0, "f32", 6,
+                    "compiled-executor merge level: 1024 walkers x 32 node pairs, merge_dim 1536 (48 x 32), "
+                    "merge_rank 1024: quadrilinear merge + residual factorized apply", cpu_sample=8,
+                    metric=EXECUTOR_METRIC),
     # The large-N evaluation forward (noncausal_bias_mha via pallas_rectangular_edge_attention):
     # one system, all queries against all keys, dense [Nq, Nk, H] bias.
     "rect": Config("rect", 1, 4096, 16, 64, 4000, 0, "f32", 5,
@@ -464,6 +473,90 @@ def run_rect(args, cfg):
     return 0
 
 
+def run_executor(args, cfg):
+    """Bench leg of one compiled-executor tree level (hz_quadrilinear_merge, hz_factorized_apply).
+    Config fields: B walkers, N node pairs (width), H groups, D rank d_r, n_phys merge_rank."""
+    import torch
+
+    from hamiltonzero_amd import _native
+
+    lib = _native.lib()
+    dev = torch.device("cuda:0")
+    B, W, G, R, Rm = cfg.B, cfg.N, cfg.H, cfg.D, cfg.n_phys
+    dm = G * R
+    M = B * W
+    rng = np.random.default_rng(cfg.seed)
+
+    def draw(shape, scale):
+        return rng.standard_normal(shape, dtype=np.float32) * np.float32(scale)
+
+    host = {"T": draw((G, R, R, R), 1.0 / R), "ul": draw((M, dm), 1.0), "ur": draw((M, dm), 1.0),
+            "V": draw((dm, Rm), dm ** -0.5), "U": draw((Rm, dm), Rm ** -0.5), "h": draw((W, Rm), 1.0)}
+    d = {k: torch.from_numpy(v).to(dev) for k, v in host.items()}
+    raw = torch.empty((M, dm), dtype=torch.float32, device=dev)
+    out = torch.empty_like(raw)
+    work = torch.empty((M, Rm), dtype=torch.float32, device=dev)
+    s = torch.cuda.current_stream(dev).cuda_stream
+    P = lambda t: t.data_ptr()  # noqa: E731
+
+    def merge(i):
+        _native.check(lib.hz_quadrilinear_merge(s, P(d["T"]), P(d["ul"]), P(d["ur"]), P(raw), M, G, R))
+
+    def apply(i):
+        _native.check(lib.hz_factorized_apply(s, P(raw), P(d["V"]), P(d["h"]), P(d["U"]), P(raw), P(out), P(work),
+                                              M, dm, Rm, dm, W))
+
+    def step(i):
+        merge(i)
+        apply(i)
+
+    stream = torch.cuda.current_stream(dev)
+    ms = timed(step, args.steps, args.warmup, stream)
+    t_s = ms / 1e3
+    merge_flops = 2 * M * G * R ** 3
+    apply_flops = 2 * M * (dm * Rm + Rm * dm)
+    flops = merge_flops + apply_flops
+    bytes_ = 4 * (3 * M * dm + G * R ** 3 + 2 * dm * Rm + W * Rm)  # u_left, u_right, out; T, V, U, h
+    # The dominant kernel, the merge, timed on its own over the same number of launches.
+    ms_merge = timed(merge, args.steps, args.warmup, stream)
+    ms_apply = timed(apply, args.steps, args.warmup, stream)
+    roof = roofline(4 * (3 * M * dm + G * R ** 3), merge_flops, ms_merge / 1e3, "f32")
+    roof["traffic"] = traffic_from_profile(args.config)
+    roof["kernel"] = "hz::quadrilinear_merge_kernel"
+    roof["basis"] = ("algorithmic flops of the merge launch, 2 M G d_r^3 (d_r outputs per group, each a "
+                     "contraction over the d_r^2 pairs k, l), per average launch duration")
+    roof["step"] = {"ms": ms, "flops": flops, "bytes": bytes_, "tflops": flops / t_s / 1e12,
+                    "merge_ms": ms_merge, "apply_ms": ms_apply,
+                    "apply_tflops": apply_flops / (ms_apply / 1e3) / 1e12}
+    cpu = None
+    if not args.no_cpu_baseline:
+        from oracle import cpu_baseline
+
+        n = cfg.cpu_sample
+        rows = n * W
+        r = cpu_baseline.time_executor_level(torch.from_numpy(host["T"]), torch.from_numpy(host["ul"][:rows]),
+                                             torch.from_numpy(host["ur"][:rows]), torch.from_numpy(host["V"]),
+                                             torch.from_numpy(host["U"]), torch.from_numpy(host["h"]),
+                                             budget_s=args.cpu_budget)
+        err = rel_err(out[:rows].cpu().numpy(), r["out"].numpy())
+        cpu = {"value": n * r["reps"] / r["seconds"],
+               "unit": "walkers/s", "cores": r["threads"], "kind": "port",
+               "sample": f"the first {n} walkers ({rows} node pairs) of the same inputs, {r['reps']} reps in "
+                         f"{r['seconds']:.1f} s, torch-CPU fp32 einsum + matmul ({r['cpu_model']})",
+               "host_cpus": r["host_cpus"],
+               "check": {"max_rel_err_vs_gpu": {"out": err}, "tol": 1e-5, "ok": err <= 1e-5}}
+    line = {
+        "metric": cfg.metric, "value": B / t_s, "unit": "walkers/s", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": ms, "higher_is_better": True, "scaling": "weak",
+        "vs_baseline": None, "dtype": "f32", "data": "synthetic (numpy default_rng; T ~ N(0,1)/d_r, unit carriers)",
+        "config": {"workload": f"{args.config}: {cfg.desc}", "walkers": B, "node_pairs": W, "groups": G, "d_r": R,
+                   "merge_rank": Rm},
+        "roofline": roof, "cpu_baseline": cpu,
+    }
+    print(json.dumps(line), flush=True)
+    return 0
+
+
 def main(argv=None):
     ap = argparse.ArgumentParser(description=__doc__.splitlines()[0])
     ap.add_argument("--gpus", type=int, default=1)
@@ -490,6 +583,8 @@ def main(argv=None):
     cfg = CONFIGS[args.config]
     if cfg.work == "rect":
         return run_rect(args, cfg)
+    if cfg.work == "executor":
+        return run_executor(args, cfg)
     return run_attention(args, cfg)
 
 

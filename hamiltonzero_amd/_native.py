@@ -1,4 +1,5 @@
-"""ctypes binding of ``libhz_mhsea.so`` (the C ABI declared in ``include/hz_mhsea.h``).
+"""ctypes binding of ``libhz_mhsea.so`` (the C ABI declared in ``include/hz_mhsea.h`` and
+``include/hz_executor.h``).
 
 The library is the only compute path of this package: there is no CPU fallback. A
 missing library raises :class:`NativeLibraryMissing` on first use.
@@ -25,7 +26,7 @@ HZ_ENULL = 2
 HZ_EALIGN = 3
 HZ_ELAUNCH = 4
 
-# Every symbol include/hz_mhsea.h declares.
+# Every symbol the headers in include/ declare.
 EXPORTED_SYMBOLS = (
     "hz_version",
     "hz_last_error",
@@ -35,6 +36,8 @@ EXPORTED_SYMBOLS = (
     "hz_mhsea_fwd_jvp_gated",
     "hz_mhsea_bwd",
     "hz_rect_attention_fwd",
+    "hz_quadrilinear_merge",
+    "hz_factorized_apply",
 )
 
 
@@ -85,6 +88,10 @@ _SIGNATURES = {
     ),
     # stream, q, k, v, bias, key_mask, out, B, Nq, Nk, H, D, scale
     "hz_rect_attention_fwd": ([_P, _P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _F], _INT),
+    # stream, T, u_a, u_b, out, M, G, R
+    "hz_quadrilinear_merge": ([_P, _P, _P, _P, _P, _I64, _I64, _I64], _INT),
+    # stream, x, V, h, U, residual, y, workspace, M, d_in, R, d_out, h_rows
+    "hz_factorized_apply": ([_P, _P, _P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64], _INT),
 }
 
 

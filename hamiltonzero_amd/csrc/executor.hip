@@ -1,0 +1,254 @@
+// The compiled per-walker executor's products on the float32 matrix cores
+// (v_mfma_f32_16x16x4_f32): the quadrilinear merge of the tree levels and the factorized
+// apply ((x V) o h) U of the leaf, merge and readout factors.
+//
+// Quadrilinear merge, out[m, iR + j] = sum_{k,l} T[i, j, k, l] a[m, iR + k] b[m, iR + l]:
+// for one group i it is one GEMM with a contraction of length R^2 = 1024,
+//     out_i[m, j] = sum_kl P_i[m, kl] T_i[kl, j],     P_i[m, kl] = a[m, iR + k] b[m, iR + l],
+// whose left operand P_i is never materialised: a lane holds its row's 32 values of a and 8
+// values of b and forms each operand value with one multiply right before its product.
+// A workgroup owns one group i, one half of the 32 outputs j and 256 rows; T_i's half
+// (1024 x 16 floats, 64 KiB) is staged in LDS once and read by every product step (one
+// 4-byte read feeds the four 16-row tiles of a wave). Two workgroups per compute unit.
+//
+// Factorized apply: two launches of one tiled GEMM, C = A B with A [M, K], B [K, N]
+// row-major; the first multiplies its result by the conditioner row of each output row
+// (h[m mod h_rows], one row per tree node, broadcast over walkers) before storing, the
+// second optionally adds a residual (the merge level's raw + apply(raw)). 128 x 128 output
+// tiles per 256-thread workgroup, 16-deep K slices double-buffered through LDS.
+#include <hip/hip_runtime.h>
+
+#include "mhsea_device.h"
+#include "mhsea_launch.h"
+
+namespace hz {
+namespace {
+
+// --------------------------------------------------------------------------------------
+// Quadrilinear merge (R = 32)
+// --------------------------------------------------------------------------------------
+constexpr int kQR = 32;            // rank of the merge tensor
+constexpr int kQRows = 256;        // rows per workgroup (4 waves x 4 tiles of 16)
+constexpr int kQHalf = 16;         // outputs j per workgroup
+constexpr int kQKL = kQR * kQR;    // contraction length
+
+__global__ void __launch_bounds__(256, 2)
+quadrilinear_merge_kernel(const float* __restrict__ T, const float* __restrict__ ua, const float* __restrict__ ub,
+                          float* __restrict__ out, int64_t M, int G) {
+  __shared__ float Ts[kQKL * kQHalf];  // Ts[kl][jj] = T[i][16 jh + jj][k][l], kl = 32 k + l
+  const int tid = threadIdx.x;
+  const int lane = tid & 63, wave = tid >> 6;
+  const int g = lane >> 4, c = lane & 15;
+  const int i = blockIdx.y;
+  const int jh = blockIdx.z;
+  const int64_t row0 = static_cast<int64_t>(blockIdx.x) * kQRows + wave * 64;
+  const int64_t ld = static_cast<int64_t>(G) * kQR;  // floats per row of a, b, out
+
+  // stage T_i's half: thread t takes output jj = t mod 16 and 4 consecutive kl per pass
+  const float* Ti = T + (static_cast<int64_t>(i) * kQR + kQHalf * jh) * kQKL;
+  for (int base = 0; base < kQKL * kQHalf / 4; base += 256) {
+    const int it = base + tid;
+    const int jj = it & 15, kl4 = it >> 4;
+    const float4 v = *reinterpret_cast<const float4*>(Ti + static_cast<int64_t>(jj) * kQKL + 4 * kl4);
+    Ts[(4 * kl4 + 0) * kQHalf + jj] = v.x;
+    Ts[(4 * kl4 + 1) * kQHalf + jj] = v.y;
+    Ts[(4 * kl4 + 2) * kQHalf + jj] = v.z;
+    Ts[(4 * kl4 + 3) * kQHalf + jj] = v.w;
+  }
+
+  // this lane's rows (one per 16-row tile): all 32 values of a, and b at l = 4 m + g
+  float a[4][kQR], b[4][8];
+#pragma unroll
+  for (int rt = 0; rt < 4; ++rt) {
+    const int64_t row = row0 + 16 * rt + c;
+    const bool ok = row < M;
+    const float* ar = ua + (ok ? row : 0) * ld + i * kQR;
+    const float* br = ub + (ok ? row : 0) * ld + i * kQR;
+#pragma unroll
+    for (int q = 0; q < kQR / 4; ++q) {
+      const float4 v = ok ? *reinterpret_cast<const float4*>(ar + 4 * q) : make_float4(0.f, 0.f, 0.f, 0.f);
+      a[rt][4 * q] = v.x;
+      a[rt][4 * q + 1] = v.y;
+      a[rt][4 * q + 2] = v.z;
+      a[rt][4 * q + 3] = v.w;
+    }
+#pragma unroll
+    for (int m = 0; m < 8; ++m) b[rt][m] = ok ? br[4 * m + g] : 0.f;
+  }
+  __syncthreads();
+
+  // step t contracts kl = 4 t + g, i.e. k = t / 8, l = 4 (t mod 8) + g
+  v4f acc[4];
+#pragma unroll
+  for (int rt = 0; rt < 4; ++rt) acc[rt] = zero4();
+#pragma unroll
+  for (int k = 0; k < kQR; ++k) {
+#pragma unroll
+    for (int m = 0; m < 8; ++m) {
+      const float tb = Ts[(32 * k + 4 * m + g) * kQHalf + c];
+#pragma unroll
+      for (int rt = 0; rt < 4; ++rt) acc[rt] = mfma16x4(a[rt][k] * b[rt][m], tb, acc[rt]);
+    }
+  }
+
+  // lane (g, c) holds out[row0 + 16 rt + 4 g + r][i R + 16 jh + c]
+#pragma unroll
+  for (int rt = 0; rt < 4; ++rt)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int64_t row = row0 + 16 * rt + 4 * g + r;
+      if (row < M) out[row * ld + i * kQR + kQHalf * jh + c] = acc[rt][r];
+    }
+}
+
+// --------------------------------------------------------------------------------------
+// Tiled GEMM with epilogues
+// --------------------------------------------------------------------------------------
+constexpr int kBM = 128, kBN = 128, kBK = 16;
+// Row lengths of As[k][row] and Bs[k][col] (floats): 16 more than a tile, so the four k rows
+// of one operand read (lanes 16 g + c read row g, column c) fall on distinct banks.
+constexpr int kAPad = kBM + 16;
+constexpr int kBPad = kBN + 16;
+
+enum GemmEpi { kEpiPlain = 0, kEpiCond = 1, kEpiResidual = 2 };
+
+// C[M, N] = A[M, K] B[K, N] (row-major); EPI: kEpiCond multiplies C[m, n] by
+// h[(m mod h_rows) * N + n]; kEpiResidual adds res[m, n]. VEC: K and N are multiples of 4
+// (16-byte staging loads); otherwise the staging loads are per element.
+template <int EPI, bool VEC>
+__global__ void __launch_bounds__(256, 2)
+gemm_f32_kernel(const float* __restrict__ A, const float* __restrict__ Bm, float* __restrict__ C,
+                const float* __restrict__ aux, int64_t M, int N, int K, int h_rows) {
+  __shared__ float As[2][kBK][kAPad];
+  __shared__ float Bs[2][kBK][kBPad];
+  const int tid = threadIdx.x;
+  const int lane = tid & 63, wave = tid >> 6;
+  const int g = lane >> 4, c = lane & 15;
+  const int64_t m0 = static_cast<int64_t>(blockIdx.y) * kBM;
+  const int n0 = blockIdx.x * kBN;
+  const int wm = (wave >> 1) * 64, wn = (wave & 1) * 64;  // this wave's 64 x 64 sub-tile
+
+  // global -> register staging: A tile 128 x 16 as 512 float4 (row = it / 4, k4 = it % 4),
+  // B tile 16 x 128 as 512 float4 (k = it / 32, n4 = it % 32); two of each per thread
+  float4 ra[2], rb[2];
+  auto gload = [&](int k0) {
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+      const int it = tid + 256 * u;
+      const int64_t row = m0 + (it >> 2);
+      const int kk = k0 + 4 * (it & 3);
+      if constexpr (VEC) {
+        ra[u] = (row < M && kk < K) ? *reinterpret_cast<const float4*>(A + row * K + kk)
+                                    : make_float4(0.f, 0.f, 0.f, 0.f);
+      } else {
+        const float* ar = A + (row < M ? row : 0) * K;
+        ra[u].x = (row < M && kk < K) ? ar[kk] : 0.f;
+        ra[u].y = (row < M && kk + 1 < K) ? ar[kk + 1] : 0.f;
+        ra[u].z = (row < M && kk + 2 < K) ? ar[kk + 2] : 0.f;
+        ra[u].w = (row < M && kk + 3 < K) ? ar[kk + 3] : 0.f;
+      }
+      const int kb = k0 + (it >> 5);
+      const int nn = n0 + 4 * (it & 31);
+      if constexpr (VEC) {
+        rb[u] = (kb < K && nn < N) ? *reinterpret_cast<const float4*>(Bm + static_cast<int64_t>(kb) * N + nn)
+                                   : make_float4(0.f, 0.f, 0.f, 0.f);
+      } else {
+        const float* br = Bm + static_cast<int64_t>(kb < K ? kb : 0) * N;
+        rb[u].x = (kb < K && nn < N) ? br[nn] : 0.f;
+        rb[u].y = (kb < K && nn + 1 < N) ? br[nn + 1] : 0.f;
+        rb[u].z = (kb < K && nn + 2 < N) ? br[nn + 2] : 0.f;
+        rb[u].w = (kb < K && nn + 3 < N) ? br[nn + 3] : 0.f;
+      }
+    }
+  };
+  auto sstore = [&](int buf) {
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+      const int it = tid + 256 * u;
+      const int r = it >> 2, k4 = 4 * (it & 3);
+      As[buf][k4 + 0][r] = ra[u].x;
+      As[buf][k4 + 1][r] = ra[u].y;
+      As[buf][k4 + 2][r] = ra[u].z;
+      As[buf][k4 + 3][r] = ra[u].w;
+      *reinterpret_cast<float4*>(&Bs[buf][it >> 5][4 * (it & 31)]) = rb[u];
+    }
+  };
+
+  v4f acc[4][4];
+#pragma unroll
+  for (int mt = 0; mt < 4; ++mt)
+#pragma unroll
+    for (int nt = 0; nt < 4; ++nt) acc[mt][nt] = zero4();
+
+  const int nk = (K + kBK - 1) / kBK;
+  gload(0);
+  sstore(0);
+  __syncthreads();
+  for (int kt = 0; kt < nk; ++kt) {
+    const int buf = kt & 1;
+    if (kt + 1 < nk) gload((kt + 1) * kBK);
+#pragma unroll
+    for (int ks = 0; ks < kBK; ks += 4) {
+      float af[4], bf[4];
+#pragma unroll
+      for (int mt = 0; mt < 4; ++mt) af[mt] = As[buf][ks + g][wm + 16 * mt + c];
+#pragma unroll
+      for (int nt = 0; nt < 4; ++nt) bf[nt] = Bs[buf][ks + g][wn + 16 * nt + c];
+#pragma unroll
+      for (int mt = 0; mt < 4; ++mt)
+#pragma unroll
+        for (int nt = 0; nt < 4; ++nt) acc[mt][nt] = mfma16x4(af[mt], bf[nt], acc[mt][nt]);
+    }
+    if (kt + 1 < nk) sstore(buf ^ 1);
+    __syncthreads();
+  }
+
+  // lane (g, c) holds C[wm + 16 mt + 4 g + r][wn + 16 nt + c]
+#pragma unroll
+  for (int mt = 0; mt < 4; ++mt)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int64_t row = m0 + wm + 16 * mt + 4 * g + r;
+      if (row >= M) continue;
+#pragma unroll
+      for (int nt = 0; nt < 4; ++nt) {
+        const int col = n0 + wn + 16 * nt + c;
+        if (col >= N) continue;
+        float v = acc[mt][nt][r];
+        if constexpr (EPI == kEpiCond) v *= aux[(row % h_rows) * N + col];
+        if constexpr (EPI == kEpiResidual) v += aux[row * N + col];
+        C[row * N + col] = v;
+      }
+    }
+}
+
+template <int EPI>
+hipError_t launch_gemm(const float* A, const float* B, float* C, const float* aux, int64_t M, int N, int K,
+                       int h_rows, hipStream_t stream) {
+  const dim3 grid(static_cast<unsigned>((N + kBN - 1) / kBN), static_cast<unsigned>((M + kBM - 1) / kBM));
+  if (N % 4 == 0 && K % 4 == 0)
+    hipLaunchKernelGGL((gemm_f32_kernel<EPI, true>), grid, dim3(256), 0, stream, A, B, C, aux, M, N, K, h_rows);
+  else
+    hipLaunchKernelGGL((gemm_f32_kernel<EPI, false>), grid, dim3(256), 0, stream, A, B, C, aux, M, N, K, h_rows);
+  return hipGetLastError();
+}
+
+}  // namespace
+
+hipError_t launch_quadrilinear_merge(const float* T, const float* ua, const float* ub, float* out, int64_t M, int G,
+                                     hipStream_t stream) {
+  const dim3 grid(static_cast<unsigned>((M + kQRows - 1) / kQRows), static_cast<unsigned>(G), 2);
+  hipLaunchKernelGGL(quadrilinear_merge_kernel, grid, dim3(256), 0, stream, T, ua, ub, out, M, G);
+  return hipGetLastError();
+}
+
+hipError_t launch_factorized_apply(const float* x, const float* V, const float* h, const float* U,
+                                   const float* residual, float* y, float* work, int64_t M, int d_in, int R, int d_out,
+                                   int h_rows, hipStream_t stream) {
+  hipError_t err = launch_gemm<kEpiCond>(x, V, work, h, M, R, d_in, h_rows, stream);
+  if (err != hipSuccess) return err;
+  if (residual != nullptr) return launch_gemm<kEpiResidual>(work, U, y, residual, M, d_out, R, 1, stream);
+  return launch_gemm<kEpiPlain>(work, U, y, nullptr, M, d_out, R, 1, stream);
+}
+
+}  // namespace hz

@@ -5,6 +5,7 @@
 #include <cstdarg>
 #include <cstdio>
 
+#include "../../include/hz_executor.h"
 #include "../../include/hz_mhsea.h"
 #include "mhsea_launch.h"
 
@@ -368,6 +369,39 @@ int hz_rect_attention_fwd(hipStream_t stream, const float* q, const float* k, co
   p.H = static_cast<int>(H);
   p.scale = scale;
   return launched(hz::launch_rect_fwd(p, static_cast<int>(D), stream));
+}
+
+int hz_quadrilinear_merge(hipStream_t stream, const float* T, const float* u_a, const float* u_b, float* out,
+                          int64_t M, int64_t G, int64_t R) {
+  if (R != 32) return fail(HZ_EINVAL, "the merge rank R must be 32, got %lld", (long long)R);
+  if (M < 1 || G < 1) return fail(HZ_EINVAL, "M and G must be >= 1, got M=%lld G=%lld", (long long)M, (long long)G);
+  if (G > 65535) return fail(HZ_EINVAL, "G = %lld exceeds the grid limit", (long long)G);
+  if ((M + 255) / 256 > 0x7fffffffLL) return fail(HZ_EINVAL, "M = %lld exceeds the grid limit", (long long)M);
+  HZ_REQUIRE(T);
+  HZ_REQUIRE(u_a);
+  HZ_REQUIRE(u_b);
+  HZ_REQUIRE(out);
+  return launched(hz::launch_quadrilinear_merge(T, u_a, u_b, out, M, static_cast<int>(G), stream));
+}
+
+int hz_factorized_apply(hipStream_t stream, const float* x, const float* V, const float* h, const float* U,
+                        const float* residual, float* y, float* workspace, int64_t M, int64_t d_in, int64_t R,
+                        int64_t d_out, int64_t h_rows) {
+  if (M < 1 || d_in < 1 || R < 1 || d_out < 1 || h_rows < 1)
+    return fail(HZ_EINVAL, "M, d_in, R, d_out and h_rows must be >= 1");
+  if (d_in > 0x7fffffffLL || R > 0x7fffffffLL || d_out > 0x7fffffffLL || h_rows > 0x7fffffffLL)
+    return fail(HZ_EINVAL, "dimensions exceed the 32-bit range");
+  if ((M + 127) / 128 > 65535) return fail(HZ_EINVAL, "M = %lld exceeds the grid limit", (long long)M);
+  HZ_REQUIRE(x);
+  HZ_REQUIRE(V);
+  HZ_REQUIRE(h);
+  HZ_REQUIRE(U);
+  HZ_REQUIRE(y);
+  HZ_REQUIRE(workspace);
+  HZ_OPTIONAL(residual);
+  return launched(hz::launch_factorized_apply(x, V, h, U, residual, y, workspace, M, static_cast<int>(d_in),
+                                              static_cast<int>(R), static_cast<int>(d_out), static_cast<int>(h_rows),
+                                              stream));
 }
 
 }  // extern "C"

@@ -105,6 +105,15 @@ hipError_t launch_keymask_empty_fwd(const FwdParams& p, int D, int T, bool given
                                     hipStream_t stream);
 hipError_t launch_keymask_empty_bwd(const BwdParams& p, int D, int dtype, hipStream_t stream);
 
+// The compiled executor's products (executor.hip), float32. Quadrilinear merge with rank 32:
+// out[m, 32 i + j] = sum_{k,l} T[i, j, k, l] ua[m, 32 i + k] ub[m, 32 i + l] for G groups.
+hipError_t launch_quadrilinear_merge(const float* T, const float* ua, const float* ub, float* out, int64_t M, int G,
+                                     hipStream_t stream);
+// y = ((x V) o h[m mod h_rows]) U (+ residual); work holds the M x R conditioned product.
+hipError_t launch_factorized_apply(const float* x, const float* V, const float* h, const float* U,
+                                   const float* residual, float* y, float* work, int64_t M, int d_in, int R, int d_out,
+                                   int h_rows, hipStream_t stream);
+
 // Rectangular attention with a dense [B, Nq, Nk, H] bias (rect_attention.hip).
 struct RectParams {
   const float* q;      // [B, Nq, H, D]

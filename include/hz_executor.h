@@ -1,0 +1,55 @@
+/*
+ * hz_executor.h — C ABI of the compiled per-walker executor's products on MI355X (gfx950).
+ *
+ * The compiled executor (src/hamiltonzero/compiled/execute.py:80-125,
+ * compiled/model.py:140-168) evaluates the wavefunction of every walker as a tree: a leaf
+ * factorized apply, then per level a quadrilinear merge of node pairs followed by a residual
+ * factorized apply, then a readout factorized apply. These entry points run those two
+ * products for all walkers and nodes of a call at once (rows = walkers x nodes, nodes
+ * innermost). Conventions as in hz_mhsea.h: device pointers, row-major, float32 (the
+ * reference computes this path in float32: odd_dtype = jnp.float32, execute.py:25,41),
+ * enqueue-only on `stream`, nothing allocated, deterministic, 0 or an HZ_E* status with
+ * hz_last_error().
+ */
+#ifndef HZ_EXECUTOR_H
+#define HZ_EXECUTOR_H
+
+#include <stdint.h>
+#include <hip/hip_runtime_api.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/*
+ * Quadrilinear merge. Replaces quadrilinear_merge_p's impl
+ * (src/hamiltonzero/model/_custom_lap_primitives.py:36-50) and
+ * _compiled_quadrilinear_merge (src/hamiltonzero/compiled/execute.py:34-52):
+ *     out[m, i R + j] = sum_{k, l} T[i, j, k, l] u_a[m, i R + k] u_b[m, i R + l]
+ * T [G, R, R, R]; u_a, u_b, out [M, G R] (the reference's u_left / u_right rows flattened
+ * over walkers and nodes). R must be 32 (the model's d_r, config.py:21); G >= 1, M >= 1.
+ */
+int hz_quadrilinear_merge(hipStream_t stream, const float* T, const float* u_a, const float* u_b, float* out,
+                          int64_t M, int64_t G, int64_t R);
+
+/*
+ * Factorized apply with the conditioner product. Replaces _factorized_apply
+ * (src/hamiltonzero/compiled/execute.py:24-31), ((x V) * h) U, and with `residual` the
+ * merge level's raw + _factorized_apply(raw) (execute.py:104):
+ *     y[m, :] = ((x[m, :] V) o h[m mod h_rows, :]) U  (+ residual[m, :])
+ * x [M, d_in], V [d_in, R], h [h_rows, R] (one conditioner row per tree node, broadcast over
+ * the walkers: rows are walkers x nodes with nodes innermost, h_rows = nodes; h_rows = 1 for
+ * the readout), U [R, d_out], residual [M, d_out] or NULL, y [M, d_out].
+ * workspace: M * R floats, caller-owned (holds the conditioned product (x V) o h).
+ * Any d_in, R, d_out >= 1 (multiples of 4 take the 16-byte staging path; the readout's
+ * d_out = 2, re and im, the per-element one).
+ */
+int hz_factorized_apply(hipStream_t stream, const float* x, const float* V, const float* h, const float* U,
+                        const float* residual, float* y, float* workspace, int64_t M, int64_t d_in, int64_t R,
+                        int64_t d_out, int64_t h_rows);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* HZ_EXECUTOR_H */

@@ -180,3 +180,33 @@ def time_rect_queries_per_s(q, k, v, bias, key_mask, scale, budget_s: float = 15
         "host_cpus": host_cpus(),
         "out": out,
     }
+
+
+def executor_level(T, ul, ur, V, U, h):
+    """One compiled-executor level's products in torch-CPU float32: the quadrilinear merge
+    (einsum, _custom_lap_primitives.py:45-50) and the residual factorized apply
+    (execute.py:24-31,104); rows are walkers x nodes, nodes innermost."""
+    G, R = T.shape[0], T.shape[1]
+    a = ul.reshape(-1, G, R)
+    b = ur.reshape(-1, G, R)
+    raw = torch.einsum("ijkl,Bik,Bil->Bij", T, a, b).reshape(ul.shape)
+    W = h.shape[0]
+    mixed = (raw @ V).reshape(-1, W, V.shape[1]) * h
+    return raw + (mixed.reshape(raw.shape[0], -1) @ U)
+
+
+def time_executor_level(T, ul, ur, V, U, h, budget_s: float = 15.0, threads: int | None = None) -> dict:
+    """Time ``executor_level`` on the given rows; returns reps / seconds and the output."""
+    threads = threads or default_threads()
+    torch.set_num_threads(threads)
+    with torch.no_grad():
+        out = executor_level(T, ul, ur, V, U, h)  # warm-up
+        reps, t0 = 0, time.perf_counter()
+        while True:
+            out = executor_level(T, ul, ur, V, U, h)
+            reps += 1
+            el = time.perf_counter() - t0
+            if el >= budget_s or reps >= 100000:
+                break
+    return {"reps": reps, "seconds": el, "threads": threads, "cpu_model": host_cpu_model(), "host_cpus": host_cpus(),
+            "out": out}

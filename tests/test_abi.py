@@ -9,11 +9,11 @@ import pytest
 
 from hamiltonzero_amd import _native
 
-HEADER = Path(__file__).resolve().parents[1] / "include" / "hz_mhsea.h"
+HEADERS = sorted((Path(__file__).resolve().parents[1] / "include").glob("*.h"))
 
 
 def header_functions():
-    text = HEADER.read_text()
+    text = "\n".join(h.read_text() for h in HEADERS)
     return sorted(set(re.findall(r"^\s*(?:int|const char\*)\s+(hz_\w+)\s*\(", text, flags=re.M)))
 
 
@@ -177,3 +177,16 @@ def test_gated_rejects_bad_arguments(lib):
         assert call(**over) == code, over
         assert needle in lib.hz_last_error().decode(), over
     assert len(lib.hz_mhsea_fwd_jvp_gated.argtypes) == 19
+
+
+def test_executor_entries_reject_bad_arguments(lib):
+    qm = lib.hz_quadrilinear_merge
+    assert qm(None, A, A, A, A, 64, 48, 16) == _native.HZ_EINVAL and b"rank" in lib.hz_last_error()
+    assert qm(None, A, A, A, A, 0, 48, 32) == _native.HZ_EINVAL
+    assert qm(None, None, A, A, A, 64, 48, 32) == _native.HZ_ENULL
+    assert qm(None, A, A + 4, A, A, 64, 48, 32) == _native.HZ_EALIGN
+    fa = lib.hz_factorized_apply
+    assert fa(None, A, A, A, A, None, A, A, 64, 0, 1024, 1536, 32) == _native.HZ_EINVAL
+    assert fa(None, A, A, A, A, None, A, None, 64, 1536, 1024, 1536, 32) == _native.HZ_ENULL
+    assert fa(None, A, A, A, A, A + 8, A, A, 64, 1536, 1024, 1536, 32) == _native.HZ_EALIGN
+    assert fa(None, A, A, A, A, None, A, A, 64, 1536, 1024, 1536, 0) == _native.HZ_EINVAL

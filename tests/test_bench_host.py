@@ -55,3 +55,10 @@ def test_multi_gpu_request_is_refused():
                        timeout=120)
     assert r.returncode == 2
     assert "one GPU" in r.stderr
+
+
+def test_merge_level_config_is_fine_tune_shaped():
+    """The executor bench leg runs one tree level at the fine-tune ranks (config.py:21-29):
+    48 groups of d_r = 32 (merge_dim 1536), merge_rank 1024, 1024 walkers x 32 node pairs."""
+    cfg = bench.CONFIGS["merge"]
+    assert (cfg.work, cfg.B, cfg.N, cfg.H, cfg.D, cfg.n_phys) == ("executor", 1024, 32, 48, 32, 1024)
