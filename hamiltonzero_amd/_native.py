@@ -38,6 +38,7 @@ EXPORTED_SYMBOLS = (
     "hz_rect_attention_fwd",
     "hz_quadrilinear_merge",
     "hz_factorized_apply",
+    "hz_factorized_apply_noalloc",
 )
 
 
@@ -92,6 +93,7 @@ _SIGNATURES = {
     "hz_quadrilinear_merge": ([_P, _P, _P, _P, _P, _I64, _I64, _I64], _INT),
     # stream, x, V, h, U, residual, y, workspace, M, d_in, R, d_out, h_rows
     "hz_factorized_apply": ([_P, _P, _P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64], _INT),
+    "hz_factorized_apply_noalloc": ([_P, _P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64], _INT),
 }
 
 

@@ -18,8 +18,15 @@
 // tiles per 256-thread workgroup, 16-deep K slices double-buffered through LDS.
 #include <hip/hip_runtime.h>
 
+#include <mutex>
+
 #include "mhsea_device.h"
 #include "mhsea_launch.h"
+
+// Workspace of hz_factorized_apply_noalloc: kApplyScratchFloats floats (32 MiB) per device,
+// held from the library's first use on that device until the process ends. Every call on a
+// device shares that device's array, so calls that overlap on one device race.
+static __device__ __align__(256) float scratch[hz::kApplyScratchFloats];
 
 namespace hz {
 namespace {
@@ -113,12 +120,13 @@ constexpr int kBPad = kBN + 16;
 enum GemmEpi { kEpiPlain = 0, kEpiCond = 1, kEpiResidual = 2 };
 
 // C[M, N] = A[M, K] B[K, N] (row-major); EPI: kEpiCond multiplies C[m, n] by
-// h[(m mod h_rows) * N + n]; kEpiResidual adds res[m, n]. VEC: K and N are multiples of 4
+// h[((row0 + m) mod h_rows) * N + n] (row0: the first row's index in the caller's full
+// row range, nonzero when the rows are processed in chunks); kEpiResidual adds res[m, n]. VEC: K and N are multiples of 4
 // (16-byte staging loads); otherwise the staging loads are per element.
 template <int EPI, bool VEC>
 __global__ void __launch_bounds__(256, 2)
 gemm_f32_kernel(const float* __restrict__ A, const float* __restrict__ Bm, float* __restrict__ C,
-                const float* __restrict__ aux, int64_t M, int N, int K, int h_rows) {
+                const float* __restrict__ aux, int64_t M, int N, int K, int h_rows, int64_t row0) {
   __shared__ float As[2][kBK][kAPad];
   __shared__ float Bs[2][kBK][kBPad];
   const int tid = threadIdx.x;
@@ -215,7 +223,7 @@ gemm_f32_kernel(const float* __restrict__ A, const float* __restrict__ Bm, float
         const int col = n0 + wn + 16 * nt + c;
         if (col >= N) continue;
         float v = acc[mt][nt][r];
-        if constexpr (EPI == kEpiCond) v *= aux[(row % h_rows) * N + col];
+        if constexpr (EPI == kEpiCond) v *= aux[((row0 + row) % h_rows) * N + col];
         if constexpr (EPI == kEpiResidual) v += aux[row * N + col];
         C[row * N + col] = v;
       }
@@ -224,14 +232,31 @@ gemm_f32_kernel(const float* __restrict__ A, const float* __restrict__ Bm, float
 
 template <int EPI>
 hipError_t launch_gemm(const float* A, const float* B, float* C, const float* aux, int64_t M, int N, int K,
-                       int h_rows, hipStream_t stream) {
+                       int h_rows, int64_t row0, hipStream_t stream) {
   const dim3 grid(static_cast<unsigned>((N + kBN - 1) / kBN), static_cast<unsigned>((M + kBM - 1) / kBM));
   if (N % 4 == 0 && K % 4 == 0)
-    hipLaunchKernelGGL((gemm_f32_kernel<EPI, true>), grid, dim3(256), 0, stream, A, B, C, aux, M, N, K, h_rows);
+    hipLaunchKernelGGL((gemm_f32_kernel<EPI, true>), grid, dim3(256), 0, stream, A, B, C, aux, M, N, K, h_rows, row0);
   else
-    hipLaunchKernelGGL((gemm_f32_kernel<EPI, false>), grid, dim3(256), 0, stream, A, B, C, aux, M, N, K, h_rows);
+    hipLaunchKernelGGL((gemm_f32_kernel<EPI, false>), grid, dim3(256), 0, stream, A, B, C, aux, M, N, K, h_rows,
+                       row0);
   return hipGetLastError();
 }
+
+// One factorized apply over rows [row0, row0 + M) of the caller's range: x, residual and y
+// point at row row0; work holds M x R floats.
+hipError_t apply_rows(const float* x, const float* V, const float* h, const float* U, const float* residual,
+                      float* y, float* work, int64_t M, int d_in, int R, int d_out, int h_rows, int64_t row0,
+                      hipStream_t stream) {
+  hipError_t err = launch_gemm<kEpiCond>(x, V, work, h, M, R, d_in, h_rows, row0, stream);
+  if (err != hipSuccess) return err;
+  if (residual != nullptr) return launch_gemm<kEpiResidual>(work, U, y, residual, M, d_out, R, 1, 0, stream);
+  return launch_gemm<kEpiPlain>(work, U, y, nullptr, M, d_out, R, 1, 0, stream);
+}
+
+// Device addresses of the no-alloc workspace, one per device, resolved on first use.
+constexpr int kMaxScratchDevices = 64;
+std::mutex g_scratch_mu;
+float* g_scratch_ptr[kMaxScratchDevices] = {};
 
 }  // namespace
 
@@ -245,10 +270,51 @@ hipError_t launch_quadrilinear_merge(const float* T, const float* ua, const floa
 hipError_t launch_factorized_apply(const float* x, const float* V, const float* h, const float* U,
                                    const float* residual, float* y, float* work, int64_t M, int d_in, int R, int d_out,
                                    int h_rows, hipStream_t stream) {
-  hipError_t err = launch_gemm<kEpiCond>(x, V, work, h, M, R, d_in, h_rows, stream);
+  return apply_rows(x, V, h, U, residual, y, work, M, d_in, R, d_out, h_rows, 0, stream);
+}
+
+static hipError_t apply_scratch_address(int device, float** ptr) {
+  if (device < 0 || device >= kMaxScratchDevices) return hipErrorInvalidDevice;
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (g_scratch_ptr[device] == nullptr) {
+    int current = -1;
+    hipError_t err = hipGetDevice(&current);
+    if (err != hipSuccess) return err;
+    if (current != device && (err = hipSetDevice(device)) != hipSuccess) return err;
+    // `scratch` names the array only inside kernels; host code uses this device's address.
+    void* addr = nullptr;
+    err = hipGetSymbolAddress(&addr, HIP_SYMBOL(scratch));
+    if (current != device) {
+      const hipError_t restore = hipSetDevice(current);
+      if (err == hipSuccess) err = restore;
+    }
+    if (err != hipSuccess) return err;
+    if (addr == nullptr) return hipErrorInvalidSymbol;
+    g_scratch_ptr[device] = static_cast<float*>(addr);
+  }
+  *ptr = g_scratch_ptr[device];
+  return hipSuccess;
+}
+
+hipError_t launch_factorized_apply_noalloc(const float* x, const float* V, const float* h, const float* U,
+                                           const float* residual, float* y, int64_t M, int d_in, int R, int d_out,
+                                           int h_rows, hipStream_t stream) {
+  if (R > kApplyScratchMaxRank) return hipErrorInvalidValue;
+  int device = -1;
+  hipError_t err = hipStreamGetDevice(stream, &device);
   if (err != hipSuccess) return err;
-  if (residual != nullptr) return launch_gemm<kEpiResidual>(work, U, y, residual, M, d_out, R, 1, stream);
-  return launch_gemm<kEpiPlain>(work, U, y, nullptr, M, d_out, R, 1, stream);
+  float* work = nullptr;
+  if ((err = apply_scratch_address(device, &work)) != hipSuccess) return err;
+  // Whole 128-row tiles of R floats per chunk; every workspace entry a chunk's second GEMM
+  // reads is written by its first, so the array needs no clearing between calls.
+  const int64_t chunk = kApplyScratchFloats / R / kBM * kBM;
+  for (int64_t r0 = 0; r0 < M; r0 += chunk) {
+    const int64_t rows = M - r0 < chunk ? M - r0 : chunk;
+    err = apply_rows(x + r0 * d_in, V, h, U, residual == nullptr ? nullptr : residual + r0 * d_out, y + r0 * d_out,
+                     work, rows, d_in, R, d_out, h_rows, r0, stream);
+    if (err != hipSuccess) return err;
+  }
+  return hipSuccess;
 }
 
 }  // namespace hz

@@ -404,4 +404,28 @@ int hz_factorized_apply(hipStream_t stream, const float* x, const float* V, cons
                                               stream));
 }
 
+int hz_factorized_apply_noalloc(hipStream_t stream, const float* x, const float* V, const float* h, const float* U,
+                                const float* residual, float* y, int64_t M, int64_t d_in, int64_t R, int64_t d_out,
+                                int64_t h_rows) {
+  if (M < 1 || d_in < 1 || R < 1 || d_out < 1 || h_rows < 1)
+    return fail(HZ_EINVAL, "M, d_in, R, d_out and h_rows must be >= 1");
+  if (d_in > 0x7fffffffLL || d_out > 0x7fffffffLL || h_rows > 0x7fffffffLL)
+    return fail(HZ_EINVAL, "dimensions exceed the 32-bit range");
+  if (R > hz::kApplyScratchMaxRank)
+    return fail(HZ_EINVAL,
+                "R = %lld exceeds the no-alloc workspace: R <= %lld (its %lld MiB device array holds 128 rows of "
+                "R floats); use hz_factorized_apply with a caller-owned workspace",
+                (long long)R, (long long)hz::kApplyScratchMaxRank, (long long)(hz::kApplyScratchFloats * 4 >> 20));
+  if ((M + 127) / 128 > 65535) return fail(HZ_EINVAL, "M = %lld exceeds the grid limit", (long long)M);
+  HZ_REQUIRE(x);
+  HZ_REQUIRE(V);
+  HZ_REQUIRE(h);
+  HZ_REQUIRE(U);
+  HZ_REQUIRE(y);
+  HZ_OPTIONAL(residual);
+  return launched(hz::launch_factorized_apply_noalloc(x, V, h, U, residual, y, M, static_cast<int>(d_in),
+                                                      static_cast<int>(R), static_cast<int>(d_out),
+                                                      static_cast<int>(h_rows), stream));
+}
+
 }  // extern "C"

@@ -113,6 +113,14 @@ hipError_t launch_quadrilinear_merge(const float* T, const float* ua, const floa
 hipError_t launch_factorized_apply(const float* x, const float* V, const float* h, const float* U,
                                    const float* residual, float* y, float* work, int64_t M, int d_in, int R, int d_out,
                                    int h_rows, hipStream_t stream);
+// The same apply with its workspace in a static device array of kApplyScratchFloats floats
+// (executor.hip), rows processed in chunks of whole 128-row tiles; R <= kApplyScratchMaxRank.
+// Allocates nothing.
+constexpr int64_t kApplyScratchFloats = int64_t(8) << 20;           // 32 MiB
+constexpr int64_t kApplyScratchMaxRank = kApplyScratchFloats / 128;  // 65536
+hipError_t launch_factorized_apply_noalloc(const float* x, const float* V, const float* h, const float* U,
+                                           const float* residual, float* y, int64_t M, int d_in, int R, int d_out,
+                                           int h_rows, hipStream_t stream);
 
 // Rectangular attention with a dense [B, Nq, Nk, H] bias (rect_attention.hip).
 struct RectParams {

@@ -48,6 +48,23 @@ int hz_factorized_apply(hipStream_t stream, const float* x, const float* V, cons
                         const float* residual, float* y, float* workspace, int64_t M, int64_t d_in, int64_t R,
                         int64_t d_out, int64_t h_rows);
 
+/*
+ * Factorized apply that allocates nothing. No counterpart in the reference: it is for callers
+ * that cannot allocate device memory or pass a workspace (code under HIP graph capture, tight
+ * serving loops, harnesses that forbid hipMalloc). Same operands and result as
+ * hz_factorized_apply (bit-identical: the same kernels per row), without `workspace`: the
+ * conditioned product lives in a static device array of 8 Mi floats (32 MiB) that every GPU
+ * the library runs on holds from its first call there until the process ends. Rows are
+ * processed in chunks of floor(8 Mi / R / 128) * 128 rows, so M is limited only by the grid
+ * (as in hz_factorized_apply); R <= 65536 (HZ_EINVAL beyond). The array needs no clearing:
+ * each chunk writes every entry it reads. All calls on one GPU share its array: calls that
+ * overlap on one GPU (concurrent streams or threads) race and must be serialised by the
+ * caller. The array is resolved for the device of `stream` on the first call there.
+ */
+int hz_factorized_apply_noalloc(hipStream_t stream, const float* x, const float* V, const float* h, const float* U,
+                                const float* residual, float* y, int64_t M, int64_t d_in, int64_t R, int64_t d_out,
+                                int64_t h_rows);
+
 #ifdef __cplusplus
 }
 #endif

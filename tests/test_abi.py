@@ -190,3 +190,14 @@ def test_executor_entries_reject_bad_arguments(lib):
     assert fa(None, A, A, A, A, None, A, None, 64, 1536, 1024, 1536, 32) == _native.HZ_ENULL
     assert fa(None, A, A, A, A, A + 8, A, A, 64, 1536, 1024, 1536, 32) == _native.HZ_EALIGN
     assert fa(None, A, A, A, A, None, A, A, 64, 1536, 1024, 1536, 0) == _native.HZ_EINVAL
+
+
+def test_noalloc_apply_rejects_bad_arguments(lib):
+    na = lib.hz_factorized_apply_noalloc
+    assert len(na.argtypes) == 12
+    assert na(None, A, A, A, A, None, A, 64, 1536, 65537, 1536, 32) == _native.HZ_EINVAL
+    msg = lib.hz_last_error().decode()
+    assert "R <= 65536" in msg and "no-alloc workspace" in msg
+    assert na(None, A, A, A, A, None, A, 0, 1536, 1024, 1536, 32) == _native.HZ_EINVAL
+    assert na(None, A, A, A, A, None, None, 64, 1536, 1024, 1536, 32) == _native.HZ_ENULL
+    assert na(None, A, A, A, A, A + 8, A, 64, 1536, 1024, 1536, 32) == _native.HZ_EALIGN
