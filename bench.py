@@ -13,7 +13,8 @@ Beside the hot path (never the default line): ``c2split`` (the reference's two-l
 drop-in, forward then tangent from (out, lse)), ``c2e`` (c2 with the pair bias e and its
 tangent), ``gate`` / ``gate_trunk`` (the trunk's sigmoid-gate head collapse fused), ``rect``
 (the large-N rectangular forward), ``merge`` (one tree level of the compiled per-walker
-executor: quadrilinear merge + residual factorized apply).
+executor: quadrilinear merge + residual factorized apply), ``trunk`` (the trunk's attention with
+its bias produced from the edge features by ln_edge + bias_mlp, then the gated fwd+JVP).
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--config NAME]
                        [--cpu-budget SECONDS] [--no-cpu-baseline]
@@ -37,6 +38,8 @@ GATE_METRIC = ("fwd+JVP attention with the sigmoid-gate head collapse fused, wal
                "% of MFMA/HBM roofline")
 RECT_METRIC = "rectangular large-N forward (noncausal_bias_mha) query rows/sec; % of MFMA/HBM roofline"
 EXECUTOR_METRIC = "compiled-executor merge level (quadrilinear merge + factorized apply) walkers/sec; % of MFMA roofline"
+TRUNK_METRIC = ("trunk attention with its learned pair bias (ln_edge + bias_mlp producer, then fwd+JVP with the gate "
+                "collapse), walkers/sec at B=1024,L=64; % of MFMA roofline")
 HBM_PEAK_GBS = 8000.0
 FP32_PEAK_TFLOPS = 157.3
 BF16_PEAK_TFLOPS = 2516.6
@@ -99,6 +102,13 @@ CONFIGS = {
                     "compiled-executor merge level: 1024 walkers x 32 node pairs, merge_dim 1536 (48 x 32), "
                     "merge_rank 1024: quadrilinear merge + residual factorized apply", cpu_sample=8,
                     metric=EXECUTOR_METRIC),
+    # The trunk's attention call with the bias it really receives: the coupling bias produced
+    # from the edge features (ln_edge + bias_mlp, trunk.py:89-105; edge_channels 96,
+    # bias hidden 64, config.py:28,31) and its tangent, then the gated fwd + JVP.
+    "trunk": Config("trunk", 1024, 64, 32, 16, 36, 1, "f32", 7,
+                    "the trunk's attention with its pair bias: edge [1024,64,64,96] and its tangent -> "
+                    "ln_edge + bias_mlp -> e, e_t [1024,64,32,64] -> gated fwd+JVP [1024,64,32,16] -> y, ydot "
+                    "[1024,64,16,16], 36/64 physical sites", cpu_sample=4, metric=TRUNK_METRIC),
     # The large-N evaluation forward (noncausal_bias_mha via pallas_rectangular_edge_attention):
     # one system, all queries against all keys, dense [Nq, Nk, H] bias.
     "rect": Config("rect", 1, 4096, 16, 64, 4000, 0, "f32", 5,
@@ -557,6 +567,110 @@ def run_executor(args, cfg):
     return 0
 
 
+def run_trunk(args, cfg):
+    """Bench leg of the trunk attention with its produced bias: hz_pair_bias (edge, edge_t ->
+    e, e_t in the attention layout) then hz_mhsea_fwd_jvp_gated. Config: B, N, H (kernel
+    heads), D (d_head), n_phys, T = 1; edge channels 96, bias hidden 64."""
+    import torch
+
+    from hamiltonzero_amd import _native
+
+    lib = _native.lib()
+    dev = torch.device("cuda:0")
+    B, N, H, D, n_phys, C, HID = cfg.B, cfg.N, cfg.H, cfg.D, cfg.n_phys, 96, 64
+    gain = 8 ** -0.5  # n_layers = 8 (config.py:23)
+    gen = torch.Generator(device=dev).manual_seed(cfg.seed)
+
+    def rnd(shape, scale=1.0):
+        return torch.randn(shape, generator=gen, device=dev, dtype=torch.float32) * scale
+
+    shape = (B, N, H, D)
+    d = {"q": rnd(shape, D ** -0.5), "k": rnd(shape, D ** -0.5), "v": rnd(shape),
+         "qt": rnd((1, *shape)), "kt": rnd((1, *shape)), "vt": rnd((1, *shape)),
+         "edge": rnd((B, N, N, C)), "edge_t": rnd((B, N, N, C))}
+    params = {"ln_w": 1.0 + 0.1 * rnd((C,)), "w_in": rnd((C, HID), C ** -0.5), "b_in": rnd((HID,), 0.1),
+              "w_1": rnd((HID, HID), HID ** -0.5), "b_1": rnd((HID,), 0.1), "w_2": rnd((HID, HID), HID ** -0.5),
+              "b_2": rnd((HID,), 0.1), "w_out": rnd((HID, H), HID ** -0.5), "b_out": rnd((H,), 0.1)}
+    mask = torch.zeros((B, N), dtype=torch.uint8, device=dev)
+    mask[:, :n_phys] = 1
+    d["e"] = torch.zeros((B, N, H, N), dtype=torch.float32, device=dev)
+    d["et"] = torch.zeros((1, B, N, H, N), dtype=torch.float32, device=dev)
+    d["y"] = torch.empty((B, N, H // 2, D), dtype=torch.float32, device=dev)
+    d["ty"] = torch.empty((1, B, N, H // 2, D), dtype=torch.float32, device=dev)
+    stream = torch.cuda.current_stream(dev)
+    s = stream.cuda_stream
+    P = lambda t: t.data_ptr()  # noqa: E731
+    div = float(np.sqrt(np.float32(D)))
+    names = ("ln_w", "w_in", "b_in", "w_1", "b_1", "w_2", "b_2", "w_out", "b_out")
+
+    def produce(i):
+        _native.check(lib.hz_pair_bias(s, P(d["edge"]), P(d["edge_t"]), P(mask), *(P(params[n]) for n in names),
+                                       P(d["e"]), P(d["et"]), B, N, C, HID, H, 1, gain, 1e-5, div, 0))
+
+    def attend(i):
+        _native.check(lib.hz_mhsea_fwd_jvp_gated(s, P(d["q"]), P(d["k"]), P(d["e"]), P(d["v"]), P(mask), P(d["qt"]),
+                                                 P(d["kt"]), P(d["et"]), P(d["vt"]), 1, P(d["y"]), P(d["ty"]), B, N,
+                                                 H, D, 1.0, 0))
+
+    def step(i):
+        produce(i)
+        attend(i)
+
+    ms = timed(step, args.steps, args.warmup, stream)
+    ms_prod = timed(produce, args.steps, args.warmup, stream)
+    ms_att = timed(attend, args.steps, args.warmup, stream)
+    # The producer's algorithmic work on the pairs it computes (both sites physical): the
+    # MLP's products for the primal and the tangent, edge and edge_t rows in, e and e_t out.
+    pairs_eff = B * n_phys * n_phys
+    pairs_all = B * N * N
+    fl_pair = 2 * (C * HID + 2 * HID * HID + HID * H)
+    flops_eff, flops_all = 2 * fl_pair * pairs_eff, 2 * fl_pair * pairs_all
+    bytes_eff = pairs_eff * 4 * (2 * C + 2 * H)
+    roof = roofline(bytes_eff, flops_eff, ms_prod / 1e3, "f32")
+    roof["traffic"] = traffic_from_profile(args.config)
+    roof["kernel"] = "hz::pair_bias_kernel<96,2,true>"
+    roof["basis"] = ("the producer launch: 2 x (C d_h + 2 d_h^2 + d_h H) x 2 flops per computed pair (primal and "
+                     "tangent), computed pairs = B n_phys^2 (the pairs the attention reads); bytes: edge and edge_t "
+                     "rows of those pairs in, e and e_t out")
+    roof["bytes_per_launch"] = bytes_eff
+    roof["flops_per_launch"] = flops_eff
+    roof["reference_equivalent"] = {
+        "basis": "every pair computed, as the reference's bias_mlp over the full [N, N] edge tensor does",
+        "flops": flops_all, "tflops": flops_all / (ms_prod / 1e3) / 1e12}
+    roof["step"] = {"ms": ms, "producer_ms": ms_prod, "attention_ms": ms_att}
+
+    cpu = None
+    if not args.no_cpu_baseline:
+        from oracle import cpu_baseline
+
+        n = min(cfg.cpu_sample, B)
+        host = {nm: t[:n].cpu() if nm not in ("qt", "kt", "vt") else t[0, :n].cpu()
+                for nm, t in d.items() if nm in ("q", "k", "v", "qt", "kt", "vt", "edge", "edge_t")}
+        hp = {nm: t.cpu() for nm, t in params.items()}
+        r = cpu_baseline.time_trunk_walkers_per_s(host, mask[:n].bool().cpu(), hp, gain, D,
+                                                  budget_s=args.cpu_budget)
+        errs = {"y": rel_err(d["y"][:n].cpu().numpy(), r["y"].numpy()),
+                "ty": rel_err(d["ty"][0, :n].cpu().numpy(), r["ty"].numpy())}
+        tol = 2e-5
+        cpu = {"value": r["walkers_per_s"], "unit": "walkers/s", "cores": r["threads"], "kind": "port",
+               "sample": f"the first {n} walkers of the same inputs, {r['reps']} reps in {r['seconds']:.1f} s, "
+                         f"torch-CPU fp32 port of the jnp path (ln_edge + bias_mlp over every pair, then the "
+                         f"attention and gate collapse, forward mode by torch.func.jvp) ({r['cpu_model']})",
+               "host_cpus": r["host_cpus"],
+               "check": {"max_rel_err_vs_gpu": errs, "tol": tol, "ok": all(v <= tol for v in errs.values())}}
+    line = {
+        "metric": cfg.metric, "value": B / (ms / 1e3), "unit": "walkers/s", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": ms, "higher_is_better": True, "scaling": "weak",
+        "vs_baseline": None, "dtype": "f32",
+        "data": "synthetic (torch.randn on the GPU, seeded; weights N(0, fan_in^-1/2), small random biases)",
+        "config": {"workload": f"{args.config}: {cfg.desc}", "B": B, "N": N, "H": H, "D": D, "n_phys": n_phys,
+                   "T": 1, "edge_channels": C, "bias_hidden": HID},
+        "roofline": roof, "cpu_baseline": cpu,
+    }
+    print(json.dumps(line), flush=True)
+    return 0
+
+
 def main(argv=None):
     ap = argparse.ArgumentParser(description=__doc__.splitlines()[0])
     ap.add_argument("--gpus", type=int, default=1)
@@ -585,6 +699,8 @@ def main(argv=None):
         return run_rect(args, cfg)
     if cfg.work == "executor":
         return run_executor(args, cfg)
+    if cfg.work == "trunk":
+        return run_trunk(args, cfg)
     return run_attention(args, cfg)
 
 

@@ -1,5 +1,5 @@
-"""ctypes binding of ``libhz_mhsea.so`` (the C ABI declared in ``include/hz_mhsea.h`` and
-``include/hz_executor.h``).
+"""ctypes binding of ``libhz_mhsea.so`` (the C ABI declared in ``include/hz_mhsea.h``,
+``include/hz_executor.h`` and ``include/hz_pair_bias.h``).
 
 The library is the only compute path of this package: there is no CPU fallback. A
 missing library raises :class:`NativeLibraryMissing` on first use.
@@ -39,6 +39,7 @@ EXPORTED_SYMBOLS = (
     "hz_quadrilinear_merge",
     "hz_factorized_apply",
     "hz_factorized_apply_noalloc",
+    "hz_pair_bias",
 )
 
 
@@ -94,6 +95,9 @@ _SIGNATURES = {
     # stream, x, V, h, U, residual, y, workspace, M, d_in, R, d_out, h_rows
     "hz_factorized_apply": ([_P, _P, _P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64], _INT),
     "hz_factorized_apply_noalloc": ([_P, _P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64], _INT),
+    # stream, edge, edge_t, mask, ln_w, w_in, b_in, w_1, b_1, w_2, b_2, w_out, b_out, e, e_t,
+    # B, N, C, hidden, H, T, inner_gain, eps, bias_div, flags
+    "hz_pair_bias": ([_P] * 15 + [_I64] * 6 + [_F, _F, _F, _INT], _INT),
 }
 
 

@@ -6,6 +6,7 @@
 #include <cstdio>
 
 #include "../../include/hz_executor.h"
+#include "../../include/hz_pair_bias.h"
 #include "../../include/hz_mhsea.h"
 #include "mhsea_launch.h"
 
@@ -426,6 +427,60 @@ int hz_factorized_apply_noalloc(hipStream_t stream, const float* x, const float*
   return launched(hz::launch_factorized_apply_noalloc(x, V, h, U, residual, y, M, static_cast<int>(d_in),
                                                       static_cast<int>(R), static_cast<int>(d_out),
                                                       static_cast<int>(h_rows), stream));
+}
+
+int hz_pair_bias(hipStream_t stream, const float* edge, const float* edge_t, const uint8_t* mask, const float* ln_w,
+                 const float* w_in, const float* b_in, const float* w_1, const float* b_1, const float* w_2,
+                 const float* b_2, const float* w_out, const float* b_out, float* e, float* e_t, int64_t B, int64_t N,
+                 int64_t C, int64_t hidden, int64_t H, int64_t T, float inner_gain, float eps, float bias_div,
+                 int flags) {
+  if (B < 1 || N < 1 || N > HZ_MAX_N) return fail(HZ_EINVAL, "B must be >= 1 and N in [1, %d]", HZ_MAX_N);
+  if (C != 32 && C != 64 && C != 96 && C != 128) return fail(HZ_EINVAL, "C = %lld: edge channels must be 32, 64, 96 or 128", (long long)C);
+  if (hidden != 64) return fail(HZ_EINVAL, "hidden = %lld: the bias MLP's hidden width must be 64", (long long)hidden);
+  if (H != 16 && H != 32 && H != 64) return fail(HZ_EINVAL, "H = %lld: heads must be 16, 32 or 64", (long long)H);
+  if (T != 0 && T != 1) return fail(HZ_EINVAL, "T = %lld: T must be 0 or 1", (long long)T);
+  if (flags & ~(HZ_FLAG_KEY_MASK | HZ_FLAG_E_QKH)) return fail(HZ_EINVAL, "unknown flag bits 0x%x", flags);
+  if (!std::isfinite(inner_gain) || !std::isfinite(eps) || eps < 0.0f || !std::isfinite(bias_div) || bias_div == 0.0f)
+    return fail(HZ_EINVAL, "inner_gain and bias_div must be finite (bias_div nonzero), eps finite and >= 0");
+  HZ_REQUIRE(edge);
+  HZ_OPTIONAL(mask);
+  HZ_REQUIRE(ln_w);
+  HZ_REQUIRE(w_in);
+  HZ_REQUIRE(b_in);
+  HZ_REQUIRE(w_1);
+  HZ_REQUIRE(b_1);
+  HZ_REQUIRE(w_2);
+  HZ_REQUIRE(b_2);
+  HZ_REQUIRE(w_out);
+  HZ_REQUIRE(b_out);
+  HZ_REQUIRE(e);
+  if (T == 1) {
+    HZ_REQUIRE(edge_t);
+    HZ_REQUIRE(e_t);
+  }
+  hz::PairBiasParams p{};
+  p.edge = edge;
+  p.edge_t = T == 1 ? edge_t : nullptr;
+  p.mask = mask;
+  p.ln_w = ln_w;
+  p.w_in = w_in;
+  p.b_in = b_in;
+  p.w_1 = w_1;
+  p.b_1 = b_1;
+  p.w_2 = w_2;
+  p.b_2 = b_2;
+  p.w_out = w_out;
+  p.b_out = b_out;
+  p.e = e;
+  p.e_t = T == 1 ? e_t : nullptr;
+  p.B = B;
+  p.N = static_cast<int>(N);
+  set_e_strides(N, H, flags, p.e_sq, p.e_sh, p.e_sk);
+  p.gain = inner_gain;
+  p.eps = eps;
+  p.div = bias_div;
+  p.key_mask = (flags & HZ_FLAG_KEY_MASK) != 0;
+  return launched(hz::launch_pair_bias(p, static_cast<int>(C), static_cast<int>(H), T == 1, stream));
 }
 
 }  // extern "C"

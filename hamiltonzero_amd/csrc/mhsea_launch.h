@@ -122,6 +122,34 @@ hipError_t launch_factorized_apply_noalloc(const float* x, const float* V, const
                                            const float* residual, float* y, int64_t M, int d_in, int R, int d_out,
                                            int h_rows, hipStream_t stream);
 
+// Coupling-bias producer of the trunk attention (pair_bias.hip): RMS + one-block MLP +
+// 1/div per site pair, written with strides (e_sq, e_sh, e_sk) inside a walker's
+// N x N x H block; T = 1 adds the tangent along edge_t into e_t.
+struct PairBiasParams {
+  const float* edge;     // [B, N, N, C]
+  const float* edge_t;   // [B, N, N, C] or null
+  const uint8_t* mask;   // [B, N] or null
+  const float* ln_w;
+  const float* w_in;
+  const float* b_in;
+  const float* w_1;
+  const float* b_1;
+  const float* w_2;
+  const float* b_2;
+  const float* w_out;
+  const float* b_out;
+  float* e;
+  float* e_t;
+  int64_t B;
+  int N;
+  int64_t e_sq, e_sh, e_sk;
+  float gain, eps, div;
+  bool key_mask;        // compute every query row (key-mask attention semantics)
+  int parts;            // items per walker (set by the launcher)
+  int64_t n_items;      // B * parts (set by the launcher)
+};
+hipError_t launch_pair_bias(PairBiasParams p, int C, int H, bool tan, hipStream_t stream);
+
 // Rectangular attention with a dense [B, Nq, Nk, H] bias (rect_attention.hip).
 struct RectParams {
   const float* q;      // [B, Nq, H, D]

@@ -1,0 +1,120 @@
+"""The trunk attention's coupling-bias producer on the gfx950 library (torch mirror).
+
+Reference: ``MultiHeadEvenAttention.__call__`` (``src/hamiltonzero/model/trunk.py:89-105``)::
+
+    edge_pre  = self.ln_edge(edge)                       # _RMS, odd_ops.py:183-215
+    coup_bias = self.bias_mlp(edge_pre)                  # UnnormalizedMLP, odd_ops.py:279-316
+    coup_bias = coup_bias / sqrt(d_head)
+
+``coupling_bias`` runs all three in one launch of ``hz_pair_bias`` (``include/hz_pair_bias.h``)
+and writes the result straight into the attention's bias layout (``[B, N, H, N]``, or the
+reference's ``[B, N, N, H]`` with ``e_layout="qkh"``), with the forward-mode tangent along
+``edge_t`` when given. There is no CPU fallback: the HIP library is required and every
+operand must be a float32 CUDA tensor on one device.
+
+Parameters use the reference's names, flattened: ``ln_w`` (``ln_edge.weight``), ``w_in`` /
+``b_in`` (``bias_mlp.in_proj``), ``w_1`` / ``b_1`` and ``w_2`` / ``b_2``
+(``bias_mlp.block_l1s[0]`` / ``block_l2s[0]``), ``w_out`` / ``b_out``
+(``bias_mlp.out_proj``); weights are ``[in, out]`` as in ``Linear`` (``odd_ops.py:78-87``).
+"""
+
+from __future__ import annotations
+
+from typing import Mapping, Optional, Tuple, Union
+
+import torch
+
+from . import _native
+
+Tensor = torch.Tensor
+
+PARAM_NAMES = ("ln_w", "w_in", "b_in", "w_1", "b_1", "w_2", "b_2", "w_out", "b_out")
+EDGE_CHANNELS = (32, 64, 96, 128)
+HIDDEN = 64
+HEADS = (16, 32, 64)
+
+
+def _check(name: str, t: Tensor, device: torch.device, shape) -> Tensor:
+    if t.dtype != torch.float32:
+        raise TypeError(f"{name}.dtype must be float32, got {t.dtype}")
+    if not t.is_cuda or t.device != device:
+        raise ValueError(f"{name} is on {t.device}: every operand must be on {device}")
+    if tuple(t.shape) != tuple(shape):
+        raise ValueError(f"{name} must have shape {tuple(shape)}, got {tuple(t.shape)}")
+    return t.contiguous()
+
+
+def coupling_bias(
+    edge: Tensor,
+    params: Mapping[str, Tensor],
+    *,
+    d_head: int,
+    inner_gain: float,
+    mask: Optional[Tensor] = None,
+    key_mask: bool = False,
+    e_layout: str = "qhk",
+    eps: float = 1e-5,
+    edge_t: Optional[Tensor] = None,
+) -> Union[Tensor, Tuple[Tensor, Tensor]]:
+    """``bias_mlp(ln_edge(edge)) / sqrt(d_head)`` for ``edge [B, N, N, C]``.
+
+    Returns ``e`` in the attention layout, or ``(e, e_t)`` when ``edge_t`` (``[B, N, N, C]``
+    or ``[T, B, N, N, C]``) is given, ``e_t`` then ``[T, <layout of e>]`` (or without the T
+    axis for a single direction). ``inner_gain`` is the MLP's ``n_layers ** -0.5``
+    (``trunk.py:61``). With ``mask [B, N]`` only the pairs the attention reads are computed
+    (see ``include/hz_pair_bias.h``; ``key_mask`` as in the attention call) and the others
+    are zero.
+    """
+    if edge.dim() != 4 or edge.shape[1] != edge.shape[2]:
+        raise ValueError(f"edge must be [B, N, N, C], got {tuple(edge.shape)}")
+    if e_layout not in ("qhk", "qkh"):
+        raise ValueError(f"e_layout must be 'qhk' or 'qkh', got {e_layout!r}")
+    B, N, _, C = edge.shape
+    if C not in EDGE_CHANNELS:
+        raise ValueError(f"edge channels must be one of {list(EDGE_CHANNELS)}, got {C}")
+    dev = edge.device
+    edge = _check("edge", edge, dev, edge.shape)
+    H = params["w_out"].shape[-1]
+    if H not in HEADS:
+        raise ValueError(f"heads (w_out's output width) must be one of {list(HEADS)}, got {H}")
+    shapes = {"ln_w": (C,), "w_in": (C, HIDDEN), "b_in": (HIDDEN,), "w_1": (HIDDEN, HIDDEN), "b_1": (HIDDEN,),
+              "w_2": (HIDDEN, HIDDEN), "b_2": (HIDDEN,), "w_out": (HIDDEN, H), "b_out": (H,)}
+    p = {n: _check(n, params[n], dev, shapes[n]) for n in PARAM_NAMES}
+    m = None
+    if mask is not None:
+        if tuple(mask.shape) != (B, N):
+            raise ValueError(f"mask must be [B, N] = {(B, N)}, got {tuple(mask.shape)}")
+        if not mask.is_cuda or mask.device != dev:
+            raise ValueError(f"mask is on {mask.device}: every operand must be on {dev}")
+        m = (mask != 0).to(torch.uint8).contiguous()
+    tangents = None
+    single = False
+    if edge_t is not None:
+        single = edge_t.dim() == 4
+        tangents = edge_t.unsqueeze(0) if single else edge_t
+        tangents = _check("edge_t", tangents, dev, (tangents.shape[0], B, N, N, C))
+    eshape = (B, N, H, N) if e_layout == "qhk" else (B, N, N, H)
+    alloc = torch.zeros if m is not None else torch.empty
+    e = alloc(eshape, dtype=torch.float32, device=dev)
+    T = 0 if tangents is None else tangents.shape[0]
+    e_t = alloc((T, *eshape), dtype=torch.float32, device=dev) if T else None
+    flags = (_native.HZ_FLAG_KEY_MASK if key_mask else 0) | (_native.HZ_FLAG_E_QKH if e_layout == "qkh" else 0)
+    lib = _native.lib()
+    stream = torch.cuda.current_stream(dev).cuda_stream
+    div = float(torch.sqrt(torch.tensor(float(d_head), dtype=torch.float32)))  # jnp.sqrt in float32
+    for t in range(max(T, 1)):
+        _native.check(lib.hz_pair_bias(
+            stream, edge.data_ptr(), None if T == 0 else tangents[t].data_ptr(), None if m is None else m.data_ptr(),
+            *(p[n].data_ptr() for n in PARAM_NAMES), e.data_ptr(), None if T == 0 else e_t[t].data_ptr(),
+            B, N, C, HIDDEN, H, 1 if T else 0, float(inner_gain), float(eps), div, flags))
+    if T == 0:
+        return e
+    return e, (e_t[0] if single else e_t)
+
+
+def inner_gain_for(n_layers: int) -> float:
+    """``float(n_layers) ** (-0.5)`` (``trunk.py:61``)."""
+    return float(n_layers) ** (-0.5)
+
+
+__all__ = ["coupling_bias", "inner_gain_for", "PARAM_NAMES"]

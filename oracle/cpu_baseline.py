@@ -210,3 +210,43 @@ def time_executor_level(T, ul, ur, V, U, h, budget_s: float = 15.0, threads: int
                 break
     return {"reps": reps, "seconds": el, "threads": threads, "cpu_model": host_cpu_model(), "host_cpus": host_cpus(),
             "out": out}
+
+
+def coupling_bias(edge, p, gain, d_head, eps=1e-5):
+    """ln_edge + bias_mlp + 1/sqrt(d_head) over every pair (trunk.py:89-105), float32;
+    edge [B, N, N, C] -> e [B, N, H, N] (the primitive's layout)."""
+    y = edge * (p["ln_w"] * torch.rsqrt(torch.mean(edge * edge, dim=-1, keepdim=True) + eps))
+    h0 = y @ p["w_in"] + p["b_in"]
+    u = h0 @ p["w_1"] + p["b_1"]
+    h1 = h0 + gain * ((u * torch.sigmoid(u)) @ p["w_2"] + p["b_2"])
+    bias = (h1 @ p["w_out"] + p["b_out"]) / torch.sqrt(torch.tensor(float(d_head)))
+    return bias.permute(0, 1, 3, 2)
+
+
+def trunk_attention(q, k, v, edge, mask, p, gain, d_head):
+    """The trunk's attention call with its produced bias and the gate collapse (q pre-scaled)."""
+    return gated(q, k, v, mask, coupling_bias(edge, p, gain, d_head))
+
+
+def time_trunk_walkers_per_s(inputs: dict, mask, params: dict, gain: float, d_head: int, budget_s: float = 15.0,
+                             threads: int | None = None) -> dict:
+    """Time the forward + JVP of :func:`trunk_attention` (tangents on q, k, v and edge) on
+    the walkers of ``inputs``; returns walkers/s and the last repetition's y, ydot."""
+    threads = threads or default_threads()
+    torch.set_num_threads(threads)
+    prim = tuple(inputs[n] for n in ("q", "k", "v", "edge"))
+    tans = tuple(inputs[n] for n in ("qt", "kt", "vt", "edge_t"))
+
+    def fn():
+        return torch.func.jvp(lambda a, b, c, x: trunk_attention(a, b, c, x, mask, params, gain, d_head), prim, tans)
+
+    y, ty = fn()  # warm-up
+    reps, t0 = 0, time.perf_counter()
+    while True:
+        y, ty = fn()
+        reps += 1
+        el = time.perf_counter() - t0
+        if el >= budget_s or reps >= 100000:
+            break
+    return {"walkers_per_s": prim[0].shape[0] * reps / el, "seconds": el, "reps": reps, "threads": threads,
+            "cpu_model": host_cpu_model(), "host_cpus": host_cpus(), "y": y.detach(), "ty": ty.detach()}
