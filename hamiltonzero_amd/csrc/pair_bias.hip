@@ -61,7 +61,44 @@ __device__ __forceinline__ float comp(const float4& v, int u) {
   return u == 0 ? v.x : (u == 1 ? v.y : (u == 2 ? v.z : v.w));
 }
 
-__device__ __forceinline__ float sigmoid(float u) { return 1.0f / (1.0f + expf(-u)); }
+// sigmoid(u) = 1 / (1 + 2^(-u log2 e)) on the hardware exp2 and reciprocal (about 1 ulp each;
+// the exponent's rounding adds |u| 2^-24 relative): a few instructions instead of a
+// full-precision expf and an IEEE division. u -> -inf gives 2^+inf = inf and 1/inf = 0.
+__device__ __forceinline__ float sigmoid(float u) {
+  return __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(u * -1.44269504088896341f));
+}
+
+// The pairs of lane column c in tile t (N block cb): query site qi, key site qj, valid.
+template <bool TAN>
+__device__ __forceinline__ void tile_pairs(int t, int c, int npairs, int nk, bool rows_listed, bool keys_listed,
+                                           const unsigned short* list, int qi[2], int qj[2], bool valid[2]) {
+  constexpr int TP = TAN ? 16 : 32;
+#pragma unroll
+  for (int cb = 0; cb < 2; ++cb) {
+    const int q = TAN ? TP * t + c : TP * t + 16 * cb + c;
+    valid[cb] = q < npairs;
+    const int qq = valid[cb] ? q : 0;
+    const int ii = qq / nk, jj = qq - ii * nk;
+    qi[cb] = rows_listed ? list[ii] : ii;
+    qj[cb] = keys_listed ? list[jj] : jj;
+  }
+}
+
+// This lane's quarter (C / 4 channels) of the edge rows of its pairs (T = 1: the pair's edge
+// and edge_t rows; T = 0: the rows of the two pairs).
+template <int C, bool TAN>
+__device__ __forceinline__ void load_rows(const float* edge_b, const float* edge_tb, int N, int g, const int qi[2],
+                                          const int qj[2], const bool valid[2], float4 xin[2][C / 16]) {
+#pragma unroll
+  for (int cb = 0; cb < 2; ++cb) {
+    const int src = TAN ? 0 : cb;
+    const float* row = (TAN && cb == 1 ? edge_tb : edge_b) + (static_cast<int64_t>(qi[src]) * N + qj[src]) * C +
+                       g * (C / 4);
+#pragma unroll
+    for (int v = 0; v < C / 16; ++v)
+      xin[cb][v] = valid[src] ? *reinterpret_cast<const float4*>(row + 4 * v) : make_float4(0.f, 0.f, 0.f, 0.f);
+  }
+}
 
 template <int C, int HB, bool TAN>
 __global__ void __launch_bounds__(256, 2) pair_bias_kernel(PairBiasParams p) {
@@ -107,6 +144,9 @@ __global__ void __launch_bounds__(256, 2) pair_bias_kernel(PairBiasParams p) {
   const int64_t pair_stride = static_cast<int64_t>(N) * N;
   const bool use_list = p.mask != nullptr && N <= kPBListN;
   const float inv_c = 1.0f / static_cast<float>(C);
+  // 1 / sqrt(d_head): exact for the power-of-two d_head the model uses (16), within 1 ulp of
+  // the reference's division otherwise.
+  const float inv_div = 1.0f / p.div;
   const int64_t total_waves = static_cast<int64_t>(gridDim.x) * kPBWaves;
 
   for (int64_t item = static_cast<int64_t>(blockIdx.x) * kPBWaves + wave; item < p.n_items; item += total_waves) {
@@ -145,34 +185,21 @@ __global__ void __launch_bounds__(256, 2) pair_bias_kernel(PairBiasParams p) {
     float* e_b = p.e + b * pair_stride * H;
     float* et_b = TAN ? p.e_t + b * pair_stride * H : nullptr;
 
+    // The edge rows of the item's first tile; each tile then loads the next tile's rows as
+    // soon as its first layer has consumed its own, so the loads fly under layers 2-4.
+    int qi[2], qj[2];
+    bool valid[2];
+    float4 xin[2][CG];
+    if (t0 < t1) {
+      tile_pairs<TAN>(t0, c, npairs, nk, rows_listed, keys_listed, list, qi, qj, valid);
+      load_rows<C, TAN>(edge_b, edge_tb, N, g, qi, qj, valid, xin);
+    }
     for (int t = t0; t < t1; ++t) {
       // The weight fragments are the same for every tile; an offset the compiler cannot see
       // through keeps their LDS reads inside the loop (hoisted, they would need 256 registers).
       int lz = 0;
       asm volatile("" : "+s"(lz));
       const float* W = lds + lz;
-      // ---- this lane's pairs (N block cb) and their edge rows ----
-      int qi[2], qj[2];
-      bool valid[2];
-      float4 xin[2][CG];
-#pragma unroll
-      for (int cb = 0; cb < 2; ++cb) {
-        const int q = TAN ? TP * t + c : TP * t + 16 * cb + c;
-        valid[cb] = q < npairs;
-        const int qq = valid[cb] ? q : 0;
-        const int ii = qq / nk, jj = qq - ii * nk;
-        qi[cb] = rows_listed ? list[ii] : ii;
-        qj[cb] = keys_listed ? list[jj] : jj;
-      }
-#pragma unroll
-      for (int cb = 0; cb < 2; ++cb) {
-        const int src = TAN ? 0 : cb;
-        const float* row = (TAN && cb == 1 ? edge_tb : edge_b) +
-                           (static_cast<int64_t>(qi[src]) * N + qj[src]) * C + g * C4;
-#pragma unroll
-        for (int v = 0; v < CG; ++v)
-          xin[cb][v] = valid[src] ? *reinterpret_cast<const float4*>(row + 4 * v) : make_float4(0.f, 0.f, 0.f, 0.f);
-      }
 
       // ---- layer 1: P = (x * w) W_in, with sum(x^2) and sum(x xdot) alongside ----
       v4f acc[4][2];
@@ -206,6 +233,12 @@ __global__ void __launch_bounds__(256, 2) pair_bias_kernel(PairBiasParams p) {
       const float r0 = 1.0f / sqrtf(v0);
       // T = 1: the tangent's column scale rdot; T = 0: the second pair block's scale
       const float r1 = TAN ? (2.0f * s1 * inv_c) * (-0.5f * r0 / v0) : 1.0f / sqrtf(s1 * inv_c + p.eps);
+      int nqi[2] = {qi[0], qi[1]}, nqj[2] = {qj[0], qj[1]};
+      bool nvalid[2] = {false, false};
+      if (t + 1 < t1) {
+        tile_pairs<TAN>(t + 1, c, npairs, nk, rows_listed, keys_listed, list, nqi, nqj, nvalid);
+        load_rows<C, TAN>(edge_b, edge_tb, N, g, nqi, nqj, nvalid, xin);
+      }
       v4f h0[4][2];
 #pragma unroll
       for (int m = 0; m < 4; ++m) {
@@ -310,7 +343,7 @@ __global__ void __launch_bounds__(256, 2) pair_bias_kernel(PairBiasParams p) {
           const float4 bo = lds4(W, L::kBout + 16 * m + 4 * g);
           float val[4];
 #pragma unroll
-          for (int r = 0; r < 4; ++r) val[r] = (o[m][cb][r] + (with_bias ? comp(bo, r) : 0.0f)) / p.div;
+          for (int r = 0; r < 4; ++r) val[r] = (o[m][cb][r] + (with_bias ? comp(bo, r) : 0.0f)) * inv_div;
           const int h = 16 * m + 4 * g;
           if (p.e_sh == 1) {
             *reinterpret_cast<float4*>(dst + h) = make_float4(val[0], val[1], val[2], val[3]);
@@ -319,6 +352,12 @@ __global__ void __launch_bounds__(256, 2) pair_bias_kernel(PairBiasParams p) {
             for (int r = 0; r < 4; ++r) dst[static_cast<int64_t>(h + r) * p.e_sh] = val[r];
           }
         }
+      }
+#pragma unroll
+      for (int cb = 0; cb < 2; ++cb) {
+        qi[cb] = nqi[cb];
+        qj[cb] = nqj[cb];
+        valid[cb] = nvalid[cb];
       }
     }
   }
