@@ -13,7 +13,8 @@ Beside the hot path (never the default line): ``c2split`` (the reference's two-l
 drop-in, forward then tangent from (out, lse)), ``c2e`` (c2 with the pair bias e and its
 tangent), ``gate`` / ``gate_trunk`` (the trunk's sigmoid-gate head collapse fused), ``rect``
 (the large-N rectangular forward), ``merge`` (one tree level of the compiled per-walker
-executor: quadrilinear merge + residual factorized apply), ``trunk`` (the trunk's attention with
+executor: quadrilinear merge + residual factorized apply), ``wavefn`` (the whole compiled
+per-walker wavefunction: leaf, every merge level, readout), ``trunk`` (the trunk's attention with
 its bias produced from the edge features by ln_edge + bias_mlp, then the gated fwd+JVP).
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--config NAME]
@@ -38,6 +39,8 @@ GATE_METRIC = ("fwd+JVP attention with the sigmoid-gate head collapse fused, wal
                "% of MFMA/HBM roofline")
 RECT_METRIC = "rectangular large-N forward (noncausal_bias_mha) query rows/sec; % of MFMA/HBM roofline"
 EXECUTOR_METRIC = "compiled-executor merge level (quadrilinear merge + factorized apply) walkers/sec; % of MFMA roofline"
+WAVEFN_METRIC = ("compiled per-walker wavefunction (leaf, 6 merge levels, readout -> log|psi|, phase) walkers/sec at "
+                 "B=1024, 64 sites, fine-tune ranks; % of MFMA roofline")
 TRUNK_METRIC = ("trunk attention with its learned pair bias (ln_edge + bias_mlp producer, then fwd+JVP with the gate "
                 "collapse), walkers/sec at B=1024,L=64; % of MFMA roofline")
 HBM_PEAK_GBS = 8000.0
@@ -102,6 +105,13 @@ CONFIGS = {
                     "compiled-executor merge level: 1024 walkers x 32 node pairs, merge_dim 1536 (48 x 32), "
                     "merge_rank 1024: quadrilinear merge + residual factorized apply", cpu_sample=8,
                     metric=EXECUTOR_METRIC),
+    # The whole compiled per-walker wavefunction at the fine-tune sizes (q_to_odd 4 -> 32,
+    # leaf rank 1536, merge_dim 1536 = 48 x 32, merge rank 1024, readout rank 64; 64 sites ->
+    # 6 merge levels): CompiledFinetuneWaveFunction._forward_plain (compiled/model.py:143-180).
+    "wavefn": Config("wavefn", 1024, 64, 48, 32, 1024, 0, "f32", 8,
+                     "compiled wavefunction: 1024 walkers x 64 sites, q [1024,64,4] -> leaf (rank 1536) -> 6 merge "
+                     "levels (merge_dim 1536, rank 1024) -> readout (rank 64) -> log|psi|, phase", cpu_sample=2,
+                     metric=WAVEFN_METRIC),
     # The trunk's attention call with the bias it really receives: the coupling bias produced
     # from the edge features (ln_edge + bias_mlp, trunk.py:89-105; edge_channels 96,
     # bias hidden 64, config.py:28,31) and its tangent, then the gated fwd + JVP.
@@ -671,6 +681,89 @@ def run_trunk(args, cfg):
     return 0
 
 
+def run_wavefn(args, cfg):
+    """Bench leg of the whole compiled wavefunction (hz_compiled_wavefunction, one call per
+    step). Config: B walkers, N sites, H groups G (d_m = 32 G), n_phys = merge rank."""
+    import torch
+
+    from hamiltonzero_amd import _native
+
+    lib = _native.lib()
+    dev = torch.device("cuda:0")
+    B, n, G, R_merge = cfg.B, cfg.N, cfg.H, cfg.n_phys
+    d_q, d_z, R_leaf, R_out, d_r = 4, 32, 1536, 64, 32
+    dm = G * d_r
+    gen = torch.Generator(device=dev).manual_seed(cfg.seed)
+
+    def w(i, o):
+        return torch.randn((i, o), generator=gen, device=dev) * i ** -0.5
+
+    L = n.bit_length() - 1
+    prm = {"q": torch.randn((B, n, d_q), generator=gen, device=dev), "q_weight": w(d_q, d_z),
+           "leaf_V": w(d_z, R_leaf), "leaf_U": w(R_leaf, dm),
+           "leaf_h": torch.randn((n, R_leaf), generator=gen, device=dev),
+           "merge_T": torch.randn((G, d_r, d_r, d_r), generator=gen, device=dev) / d_r,
+           "merge_V": w(dm, R_merge), "merge_U": w(R_merge, dm),
+           "merge_h": torch.randn((L, n // 2, R_merge), generator=gen, device=dev),
+           "opcodes": torch.zeros((L, n // 2), dtype=torch.uint8, device=dev),  # every node merges
+           "readout_V": w(dm, R_out), "readout_U": w(R_out, 2),
+           "readout_h": torch.randn((R_out,), generator=gen, device=dev)}
+    log_abs = torch.empty(B, device=dev)
+    phase = torch.empty(B, device=dev)
+    nbytes = lib.hz_compiled_wavefunction_workspace(B, n, d_z, R_leaf, dm, R_merge, R_out)
+    work = torch.empty(nbytes // 4 + 64, device=dev)
+    stream = torch.cuda.current_stream(dev)
+    names = ("q", "q_weight", "leaf_V", "leaf_U", "leaf_h", "merge_T", "merge_V", "merge_U", "merge_h", "opcodes",
+             "readout_V", "readout_U", "readout_h")
+
+    def step(i):
+        _native.check(lib.hz_compiled_wavefunction(stream.cuda_stream, *(prm[k].data_ptr() for k in names),
+                                                   log_abs.data_ptr(), phase.data_ptr(), work.data_ptr(), nbytes, B,
+                                                   n, d_q, d_z, R_leaf, G, d_r, R_merge, R_out, 1e-6))
+
+    ms = timed(step, args.steps, args.warmup, stream)
+    rows = B * n
+    merge_rows = B * (n - 1)  # every level's nodes: n/2 + n/4 + ... + 1 per walker
+    flops = (2 * rows * (d_q * d_z + d_z * R_leaf + R_leaf * dm)
+             + merge_rows * (2 * G * d_r ** 3 + 2 * (dm * R_merge + R_merge * dm))
+             + 2 * B * (dm * R_out + R_out * 2))
+    roof = roofline(4 * (rows * d_q + B * 2), flops, ms / 1e3, "f32")
+    roof["traffic"] = traffic_from_profile(args.config)
+    roof["kernel"] = "hz_compiled_wavefunction (every launch of the step)"
+    roof["basis"] = ("algorithmic flops of the step: the leaf GEMMs 2 B n (d_q d_z + d_z R_leaf + R_leaf d_m), per "
+                     "merged node 2 G d_r^3 + 4 d_m R_merge, the readout; per average step duration")
+    roof["flops_per_step"] = flops
+    cpu = None
+    if not args.no_cpu_baseline:
+        from oracle import cpu_baseline
+
+        k = min(cfg.cpu_sample, B)
+        host = {nm: t.cpu() for nm, t in prm.items()}
+        host["q"] = host["q"][:k]
+        r = cpu_baseline.time_wavefunction_walkers_per_s(host, 1e-6, budget_s=args.cpu_budget)
+        got_la, got_ph = log_abs[:k].cpu().double().numpy(), phase[:k].cpu().double().numpy()
+        d_la = float(np.max(np.abs(got_la - r["log_abs"].double().numpy())))
+        d_ph = float(np.max(np.abs(np.angle(np.exp(1j * (got_ph - r["phase"].double().numpy()))))))
+        tol = 1e-4
+        cpu = {"value": r["walkers_per_s"], "unit": "walkers/s", "cores": r["threads"], "kind": "port",
+               "sample": f"the first {k} walkers of the same inputs, {r['reps']} reps in {r['seconds']:.1f} s, "
+                         f"torch-CPU fp32 port of _forward_plain ({r['cpu_model']})",
+               "host_cpus": r["host_cpus"],
+               "check": {"max_abs_diff_vs_gpu": {"log_abs": d_la, "phase": d_ph}, "tol": tol,
+                         "ok": d_la <= tol * max(1.0, float(np.max(np.abs(got_la)))) and d_ph <= tol}}
+    line = {
+        "metric": cfg.metric, "value": B / (ms / 1e3), "unit": "walkers/s", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": ms, "higher_is_better": True, "scaling": "weak",
+        "vs_baseline": None, "dtype": "f32",
+        "data": "synthetic (torch.randn on the GPU, seeded; weights N(0, fan_in^-1/2); every node merges)",
+        "config": {"workload": f"{args.config}: {cfg.desc}", "walkers": B, "n_sites": n, "d_q": d_q, "d_z": d_z,
+                   "leaf_rank": R_leaf, "merge_dim": dm, "merge_rank": R_merge, "readout_rank": R_out},
+        "roofline": roof, "cpu_baseline": cpu,
+    }
+    print(json.dumps(line), flush=True)
+    return 0
+
+
 def main(argv=None):
     ap = argparse.ArgumentParser(description=__doc__.splitlines()[0])
     ap.add_argument("--gpus", type=int, default=1)
@@ -701,6 +794,8 @@ def main(argv=None):
         return run_executor(args, cfg)
     if cfg.work == "trunk":
         return run_trunk(args, cfg)
+    if cfg.work == "wavefn":
+        return run_wavefn(args, cfg)
     return run_attention(args, cfg)
 
 

@@ -39,6 +39,8 @@ EXPORTED_SYMBOLS = (
     "hz_quadrilinear_merge",
     "hz_factorized_apply",
     "hz_factorized_apply_noalloc",
+    "hz_compiled_wavefunction_workspace",
+    "hz_compiled_wavefunction",
     "hz_pair_bias",
 )
 
@@ -95,6 +97,12 @@ _SIGNATURES = {
     # stream, x, V, h, U, residual, y, workspace, M, d_in, R, d_out, h_rows
     "hz_factorized_apply": ([_P, _P, _P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64], _INT),
     "hz_factorized_apply_noalloc": ([_P, _P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64], _INT),
+    # B, n_sites, d_z, R_leaf, d_m, R_merge, R_out
+    "hz_compiled_wavefunction_workspace": ([_I64] * 7, _I64),
+    # stream, q, q_weight, leaf_V, leaf_U, leaf_h, merge_T, merge_V, merge_U, merge_h, opcodes,
+    # readout_V, readout_U, readout_h, log_abs, phase, workspace, workspace_bytes,
+    # B, n_sites, d_q, d_z, R_leaf, G, d_r, R_merge, R_out, merge_eps
+    "hz_compiled_wavefunction": ([_P] * 17 + [_I64] * 10 + [_F], _INT),
     # stream, edge, edge_t, mask, ln_w, w_in, b_in, w_1, b_1, w_2, b_2, w_out, b_out, e, e_t,
     # B, N, C, hidden, H, T, inner_gain, eps, bias_div, flags
     "hz_pair_bias": ([_P] * 15 + [_I64] * 6 + [_F, _F, _F, _INT], _INT),

@@ -41,7 +41,7 @@ constexpr int kQKL = kQR * kQR;    // contraction length
 
 __global__ void __launch_bounds__(256, 2)
 quadrilinear_merge_kernel(const float* __restrict__ T, const float* __restrict__ ua, const float* __restrict__ ub,
-                          float* __restrict__ out, int64_t M, int G) {
+                          float* __restrict__ out, int64_t M, int G, int64_t ld_in) {
   __shared__ float Ts[kQKL * kQHalf];  // Ts[kl][jj] = T[i][16 jh + jj][k][l], kl = 32 k + l
   const int tid = threadIdx.x;
   const int lane = tid & 63, wave = tid >> 6;
@@ -49,7 +49,7 @@ quadrilinear_merge_kernel(const float* __restrict__ T, const float* __restrict__
   const int i = blockIdx.y;
   const int jh = blockIdx.z;
   const int64_t row0 = static_cast<int64_t>(blockIdx.x) * kQRows + wave * 64;
-  const int64_t ld = static_cast<int64_t>(G) * kQR;  // floats per row of a, b, out
+  const int64_t ld = static_cast<int64_t>(G) * kQR;  // floats per row of out (ld_in: of a and b)
 
   // stage T_i's half: thread t takes output jj = t mod 16 and 4 consecutive kl per pass
   const float* Ti = T + (static_cast<int64_t>(i) * kQR + kQHalf * jh) * kQKL;
@@ -69,8 +69,8 @@ quadrilinear_merge_kernel(const float* __restrict__ T, const float* __restrict__
   for (int rt = 0; rt < 4; ++rt) {
     const int64_t row = row0 + 16 * rt + c;
     const bool ok = row < M;
-    const float* ar = ua + (ok ? row : 0) * ld + i * kQR;
-    const float* br = ub + (ok ? row : 0) * ld + i * kQR;
+    const float* ar = ua + (ok ? row : 0) * ld_in + i * kQR;
+    const float* br = ub + (ok ? row : 0) * ld_in + i * kQR;
 #pragma unroll
     for (int q = 0; q < kQR / 4; ++q) {
       const float4 v = ok ? *reinterpret_cast<const float4*>(ar + 4 * q) : make_float4(0.f, 0.f, 0.f, 0.f);
@@ -121,12 +121,14 @@ enum GemmEpi { kEpiPlain = 0, kEpiCond = 1, kEpiResidual = 2 };
 
 // C[M, N] = A[M, K] B[K, N] (row-major); EPI: kEpiCond multiplies C[m, n] by
 // h[((row0 + m) mod h_rows) * N + n] (row0: the first row's index in the caller's full
-// row range, nonzero when the rows are processed in chunks); kEpiResidual adds res[m, n]. VEC: K and N are multiples of 4
+// row range, nonzero when the rows are processed in chunks); kEpiResidual adds res[m, n].
+// C may be the residual itself (each output entry reads its residual entry, then overwrites
+// it, in one thread), so neither carries __restrict__. VEC: K and N are multiples of 4
 // (16-byte staging loads); otherwise the staging loads are per element.
 template <int EPI, bool VEC>
 __global__ void __launch_bounds__(256, 2)
-gemm_f32_kernel(const float* __restrict__ A, const float* __restrict__ Bm, float* __restrict__ C,
-                const float* __restrict__ aux, int64_t M, int N, int K, int h_rows, int64_t row0) {
+gemm_f32_kernel(const float* __restrict__ A, const float* __restrict__ Bm, float* C, const float* aux, int64_t M, int N,
+                int K, int h_rows, int64_t row0) {
   __shared__ float As[2][kBK][kAPad];
   __shared__ float Bs[2][kBK][kBPad];
   const int tid = threadIdx.x;
@@ -258,12 +260,185 @@ constexpr int kMaxScratchDevices = 64;
 std::mutex g_scratch_mu;
 float* g_scratch_ptr[kMaxScratchDevices] = {};
 
+// --------------------------------------------------------------------------------------
+// Row epilogues of the executor, one wave per row of d floats (d a multiple of 4,
+// d <= 64 * 4 * kRowVec): the leaf carriers' RMS normalisation, a level's rescale and
+// opcode gate, and the readout's log|psi| and phase. Each row's sum of squares is reduced
+// across the wave in a fixed order (results reproducible run to run).
+// --------------------------------------------------------------------------------------
+constexpr int kRowVec = 8;  // float4 per lane: rows up to 2048 floats
+
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off);
+  return v;
+}
+
+__device__ __forceinline__ float sum_sq(const float4& v) { return v.x * v.x + v.y * v.y + v.z * v.z + v.w * v.w; }
+
+// u[m, :] /= rms, s[m] = log(rms), rms = sqrt(mean(u[m]^2) + 1e-30)
+__global__ void __launch_bounds__(256) normalize_rows_kernel(float* __restrict__ u, float* __restrict__ s, int64_t M,
+                                                              int d) {
+  const int lane = threadIdx.x & 63;
+  const int64_t row = static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6);
+  if (row >= M) return;
+  float4* ur = reinterpret_cast<float4*>(u + row * d);
+  const int d4 = d / 4;
+  float4 v[kRowVec];
+  float ss = 0.f;
+#pragma unroll
+  for (int t = 0; t < kRowVec; ++t) {
+    const int c4 = lane + 64 * t;
+    v[t] = c4 < d4 ? ur[c4] : make_float4(0.f, 0.f, 0.f, 0.f);
+    ss += sum_sq(v[t]);
+  }
+  ss = wave_sum(ss);
+  const float rms = sqrtf(ss / static_cast<float>(d) + 1e-30f);
+#pragma unroll
+  for (int t = 0; t < kRowVec; ++t) {
+    const int c4 = lane + 64 * t;
+    if (c4 < d4) ur[c4] = make_float4(v[t].x / rms, v[t].y / rms, v[t].z / rms, v[t].w / rms);
+  }
+  if (lane == 0) s[row] = logf(rms);
+}
+
+// One tree level's epilogue for output row m = (walker, node p), M = walkers x width:
+//   scale = sqrt(mean(out[m]^2) + eps), candidate = out[m] / scale,
+//   u'[m] = both * candidate + left * u[2m] + right * u[2m + 1]   (gates from opcode[p])
+//   s'[m] = both * (s[2m] + s[2m + 1] + log(scale)) + left * s[2m] + right * s[2m + 1]
+__global__ void __launch_bounds__(256) level_gate_kernel(const float* __restrict__ out, const float* __restrict__ u_in,
+                                                          const float* __restrict__ s_in,
+                                                          const uint8_t* __restrict__ opcodes, float* __restrict__ u_out,
+                                                          float* __restrict__ s_out, int64_t M, int width, int d,
+                                                          float eps) {
+  const int lane = threadIdx.x & 63;
+  const int64_t row = static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6);
+  if (row >= M) return;
+  const int d4 = d / 4;
+  const float4* orow = reinterpret_cast<const float4*>(out + row * d);
+  const float4* lrow = reinterpret_cast<const float4*>(u_in + 2 * row * d);
+  const float4* rrow = lrow + d4;
+  float4 v[kRowVec];
+  float ss = 0.f;
+#pragma unroll
+  for (int t = 0; t < kRowVec; ++t) {
+    const int c4 = lane + 64 * t;
+    v[t] = c4 < d4 ? orow[c4] : make_float4(0.f, 0.f, 0.f, 0.f);
+    ss += sum_sq(v[t]);
+  }
+  ss = wave_sum(ss);
+  const float scale = sqrtf(ss / static_cast<float>(d) + eps);
+  const int op = opcodes[row % width];
+  const float both = op == 0 ? 1.f : 0.f, left = op == 1 ? 1.f : 0.f, right = op == 2 ? 1.f : 0.f;
+  float4* urow = reinterpret_cast<float4*>(u_out + row * d);
+#pragma unroll
+  for (int t = 0; t < kRowVec; ++t) {
+    const int c4 = lane + 64 * t;
+    if (c4 < d4) {
+      const float4 a = lrow[c4], b = rrow[c4];
+      float4 r;
+      r.x = both * (v[t].x / scale) + left * a.x + right * b.x;
+      r.y = both * (v[t].y / scale) + left * a.y + right * b.y;
+      r.z = both * (v[t].z / scale) + left * a.z + right * b.z;
+      r.w = both * (v[t].w / scale) + left * a.w + right * b.w;
+      urow[c4] = r;
+    }
+  }
+  if (lane == 0) {
+    const float sl = s_in[2 * row], sr = s_in[2 * row + 1];
+    s_out[row] = both * (sl + sr + logf(scale)) + left * sl + right * sr;
+  }
+}
+
+// log|psi| = 0.5 log(re^2 + im^2) + s_root, phase = atan2(im, re); psi [B, 2]
+__global__ void __launch_bounds__(256) readout_kernel(const float* __restrict__ psi, const float* __restrict__ s_root,
+                                                       float* __restrict__ log_abs, float* __restrict__ phase, int64_t B) {
+  const int64_t b = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
+  if (b >= B) return;
+  const float re = psi[2 * b], im = psi[2 * b + 1];
+  log_abs[b] = 0.5f * logf(re * re + im * im) + s_root[b];
+  phase[b] = atan2f(im, re);
+}
+
+// Workspace sections of the whole-wavefunction executor, in floats, each rounded up to 64
+// floats (256 bytes).
+struct WaveFnWorkspace {
+  int64_t z, work, u0, u1, raw, s0, s1, psi, total;
+  WaveFnWorkspace(int64_t B, int64_t n, int64_t d_z, int64_t r_leaf, int64_t d_m, int64_t r_merge, int64_t r_out) {
+    auto up = [](int64_t x) { return (x + 63) / 64 * 64; };
+    const int64_t half = n > 1 ? n / 2 : 1;
+    int64_t wk = B * n * r_leaf;
+    if (B * half * r_merge > wk) wk = B * half * r_merge;
+    if (B * r_out > wk) wk = B * r_out;
+    z = 0;
+    work = z + up(B * n * d_z);
+    u0 = work + up(wk);
+    u1 = u0 + up(B * n * d_m);
+    raw = u1 + up(B * half * d_m);
+    s0 = raw + up(B * half * d_m);
+    s1 = s0 + up(B * n);
+    psi = s1 + up(B * half);
+    total = psi + up(2 * B);
+  }
+};
+
 }  // namespace
 
+int64_t compiled_wavefunction_workspace_bytes(int64_t B, int64_t n, int64_t d_z, int64_t r_leaf, int64_t d_m,
+                                              int64_t r_merge, int64_t r_out) {
+  return WaveFnWorkspace(B, n, d_z, r_leaf, d_m, r_merge, r_out).total * static_cast<int64_t>(sizeof(float));
+}
+
+hipError_t launch_compiled_wavefunction(const WaveFnParams& p, hipStream_t stream) {
+  const WaveFnWorkspace L(p.B, p.n, p.d_z, p.r_leaf, p.d_m, p.r_merge, p.r_out);
+  float* ws = p.workspace;
+  float *z = ws + L.z, *work = ws + L.work, *raw = ws + L.raw, *psi = ws + L.psi;
+  float* u_buf[2] = {ws + L.u0, ws + L.u1};
+  float* s_buf[2] = {ws + L.s0, ws + L.s1};
+  const int64_t rows = p.B * p.n;
+  const int G = p.d_m / kQR;
+  hipError_t err;
+  // leaf: z = q W_q; u = ((z V) o leaf_h[site]) U; carriers RMS-normalised, s = log rms
+  if ((err = launch_gemm<kEpiPlain>(p.q, p.q_weight, z, nullptr, rows, p.d_z, p.d_q, 1, 0, stream)) != hipSuccess)
+    return err;
+  if ((err = apply_rows(z, p.leaf_V, p.leaf_h, p.leaf_U, nullptr, u_buf[0], work, rows, p.d_z, p.r_leaf, p.d_m, p.n, 0,
+                        stream)) != hipSuccess)
+    return err;
+  hipLaunchKernelGGL(normalize_rows_kernel, dim3(static_cast<unsigned>((rows + 3) / 4)), dim3(256), 0, stream,
+                     u_buf[0], s_buf[0], rows, p.d_m);
+  if ((err = hipGetLastError()) != hipSuccess) return err;
+  // levels: node pairs (2p, 2p + 1) merged into node p, widths n/2, n/4, ..., 1
+  int cur = 0;
+  for (int level = 0, width = p.n / 2; width >= 1; ++level, width /= 2) {
+    const int64_t m = p.B * width;
+    const float* u_in = u_buf[cur];
+    const float* h_level = p.merge_h + static_cast<int64_t>(level) * (p.n / 2) * p.r_merge;
+    const uint8_t* ops = p.opcodes + static_cast<int64_t>(level) * (p.n / 2);
+    if ((err = launch_quadrilinear_merge(p.merge_T, u_in, u_in + p.d_m, raw, m, G, 2 * static_cast<int64_t>(p.d_m),
+                                         stream)) != hipSuccess)
+      return err;
+    // out = raw + ((raw V) o h_level[node]) U, written over raw
+    if ((err = apply_rows(raw, p.merge_V, h_level, p.merge_U, raw, raw, work, m, p.d_m, p.r_merge, p.d_m, width, 0,
+                          stream)) != hipSuccess)
+      return err;
+    hipLaunchKernelGGL(level_gate_kernel, dim3(static_cast<unsigned>((m + 3) / 4)), dim3(256), 0, stream, raw, u_in,
+                       s_buf[cur], ops, u_buf[cur ^ 1], s_buf[cur ^ 1], m, width, p.d_m, p.merge_eps);
+    if ((err = hipGetLastError()) != hipSuccess) return err;
+    cur ^= 1;
+  }
+  // readout: psi = ((u_root V) o readout_h) U, then log|psi| and phase
+  if ((err = apply_rows(u_buf[cur], p.readout_V, p.readout_h, p.readout_U, nullptr, psi, work, p.B, p.d_m, p.r_out, 2,
+                        1, 0, stream)) != hipSuccess)
+    return err;
+  hipLaunchKernelGGL(readout_kernel, dim3(static_cast<unsigned>((p.B + 255) / 256)), dim3(256), 0, stream, psi,
+                     s_buf[cur], p.log_abs, p.phase, p.B);
+  return hipGetLastError();
+}
+
 hipError_t launch_quadrilinear_merge(const float* T, const float* ua, const float* ub, float* out, int64_t M, int G,
-                                     hipStream_t stream) {
+                                     int64_t ld_in, hipStream_t stream) {
   const dim3 grid(static_cast<unsigned>((M + kQRows - 1) / kQRows), static_cast<unsigned>(G), 2);
-  hipLaunchKernelGGL(quadrilinear_merge_kernel, grid, dim3(256), 0, stream, T, ua, ub, out, M, G);
+  hipLaunchKernelGGL(quadrilinear_merge_kernel, grid, dim3(256), 0, stream, T, ua, ub, out, M, G, ld_in);
   return hipGetLastError();
 }
 

@@ -382,7 +382,7 @@ int hz_quadrilinear_merge(hipStream_t stream, const float* T, const float* u_a, 
   HZ_REQUIRE(u_a);
   HZ_REQUIRE(u_b);
   HZ_REQUIRE(out);
-  return launched(hz::launch_quadrilinear_merge(T, u_a, u_b, out, M, static_cast<int>(G), stream));
+  return launched(hz::launch_quadrilinear_merge(T, u_a, u_b, out, M, static_cast<int>(G), G * R, stream));
 }
 
 int hz_factorized_apply(hipStream_t stream, const float* x, const float* V, const float* h, const float* U,
@@ -481,6 +481,83 @@ int hz_pair_bias(hipStream_t stream, const float* edge, const float* edge_t, con
   p.div = bias_div;
   p.key_mask = (flags & HZ_FLAG_KEY_MASK) != 0;
   return launched(hz::launch_pair_bias(p, static_cast<int>(C), static_cast<int>(H), T == 1, stream));
+}
+
+int64_t hz_compiled_wavefunction_workspace(int64_t B, int64_t n_sites, int64_t d_z, int64_t R_leaf, int64_t d_m,
+                                           int64_t R_merge, int64_t R_out) {
+  if (B < 1 || n_sites < 1 || d_z < 1 || R_leaf < 1 || d_m < 1 || R_merge < 1 || R_out < 1) return -1;
+  return hz::compiled_wavefunction_workspace_bytes(B, n_sites, d_z, R_leaf, d_m, R_merge, R_out);
+}
+
+int hz_compiled_wavefunction(hipStream_t stream, const float* q, const float* q_weight, const float* leaf_V,
+                             const float* leaf_U, const float* leaf_h, const float* merge_T, const float* merge_V,
+                             const float* merge_U, const float* merge_h, const uint8_t* opcodes, const float* readout_V,
+                             const float* readout_U, const float* readout_h, float* log_abs, float* phase,
+                             void* workspace, int64_t workspace_bytes, int64_t B, int64_t n_sites, int64_t d_q,
+                             int64_t d_z, int64_t R_leaf, int64_t G, int64_t d_r, int64_t R_merge, int64_t R_out,
+                             float merge_eps) {
+  if (B < 1 || n_sites < 1 || d_q < 1 || d_z < 1 || R_leaf < 1 || G < 1 || R_merge < 1 || R_out < 1)
+    return fail(HZ_EINVAL, "B, n_sites, d_q, d_z, R_leaf, G, R_merge and R_out must be >= 1");
+  if (n_sites & (n_sites - 1)) return fail(HZ_EINVAL, "n_sites must be a power of two, got %lld", (long long)n_sites);
+  if (d_r != 32) return fail(HZ_EINVAL, "d_r = %lld: the merge tensor's rank must be 32", (long long)d_r);
+  const int64_t d_m = G * d_r;
+  if (d_m > hz::kRowMaxFloats)
+    return fail(HZ_EINVAL, "carrier width G * d_r = %lld exceeds %d", (long long)d_m, hz::kRowMaxFloats);
+  if (n_sites > 0x7fffffffLL || d_q > 0x7fffffffLL || d_z > 0x7fffffffLL || R_leaf > 0x7fffffffLL ||
+      R_merge > 0x7fffffffLL || R_out > 0x7fffffffLL)
+    return fail(HZ_EINVAL, "dimensions exceed the 32-bit range");
+  if ((B * n_sites + 127) / 128 > 65535 || (B * n_sites + 255) / 256 > 0x7fffffffLL)
+    return fail(HZ_EINVAL, "B * n_sites = %lld exceeds the grid limit", (long long)(B * n_sites));
+  if (!std::isfinite(merge_eps) || merge_eps < 0.0f) return fail(HZ_EINVAL, "merge_eps must be finite and >= 0");
+  const int64_t need = hz::compiled_wavefunction_workspace_bytes(B, n_sites, d_z, R_leaf, d_m, R_merge, R_out);
+  if (workspace_bytes < need)
+    return fail(HZ_EINVAL, "workspace_bytes = %lld, need %lld (hz_compiled_wavefunction_workspace)",
+                (long long)workspace_bytes, (long long)need);
+  HZ_REQUIRE(q);
+  HZ_REQUIRE(q_weight);
+  HZ_REQUIRE(leaf_V);
+  HZ_REQUIRE(leaf_U);
+  HZ_REQUIRE(leaf_h);
+  HZ_REQUIRE(merge_T);
+  if (n_sites > 1) {
+    HZ_REQUIRE(merge_V);
+    HZ_REQUIRE(merge_U);
+    HZ_REQUIRE(merge_h);
+    HZ_REQUIRE(opcodes);
+  }
+  HZ_REQUIRE(readout_V);
+  HZ_REQUIRE(readout_U);
+  HZ_REQUIRE(readout_h);
+  HZ_REQUIRE(log_abs);
+  HZ_REQUIRE(phase);
+  HZ_REQUIRE(workspace);
+  hz::WaveFnParams p{};
+  p.q = q;
+  p.q_weight = q_weight;
+  p.leaf_V = leaf_V;
+  p.leaf_U = leaf_U;
+  p.leaf_h = leaf_h;
+  p.merge_T = merge_T;
+  p.merge_V = merge_V;
+  p.merge_U = merge_U;
+  p.merge_h = merge_h;
+  p.opcodes = opcodes;
+  p.readout_V = readout_V;
+  p.readout_U = readout_U;
+  p.readout_h = readout_h;
+  p.log_abs = log_abs;
+  p.phase = phase;
+  p.workspace = static_cast<float*>(workspace);
+  p.B = B;
+  p.n = static_cast<int>(n_sites);
+  p.d_q = static_cast<int>(d_q);
+  p.d_z = static_cast<int>(d_z);
+  p.r_leaf = static_cast<int>(R_leaf);
+  p.d_m = static_cast<int>(d_m);
+  p.r_merge = static_cast<int>(R_merge);
+  p.r_out = static_cast<int>(R_out);
+  p.merge_eps = merge_eps;
+  return launched(hz::launch_compiled_wavefunction(p, stream));
 }
 
 }  // extern "C"

@@ -108,7 +108,7 @@ hipError_t launch_keymask_empty_bwd(const BwdParams& p, int D, int dtype, hipStr
 // The compiled executor's products (executor.hip), float32. Quadrilinear merge with rank 32:
 // out[m, 32 i + j] = sum_{k,l} T[i, j, k, l] ua[m, 32 i + k] ub[m, 32 i + l] for G groups.
 hipError_t launch_quadrilinear_merge(const float* T, const float* ua, const float* ub, float* out, int64_t M, int G,
-                                     hipStream_t stream);
+                                     int64_t ld_in, hipStream_t stream);
 // y = ((x V) o h[m mod h_rows]) U (+ residual); work holds the M x R conditioned product.
 hipError_t launch_factorized_apply(const float* x, const float* V, const float* h, const float* U,
                                    const float* residual, float* y, float* work, int64_t M, int d_in, int R, int d_out,
@@ -116,6 +116,33 @@ hipError_t launch_factorized_apply(const float* x, const float* V, const float* 
 // The same apply with its workspace in a static device array of kApplyScratchFloats floats
 // (executor.hip), rows processed in chunks of whole 128-row tiles; R <= kApplyScratchMaxRank.
 // Allocates nothing.
+// The whole per-walker wavefunction of the compiled executor (leaf, every merge level,
+// readout) on one stream; workspace of compiled_wavefunction_workspace_bytes().
+struct WaveFnParams {
+  const float* q;          // [B, n, d_q]
+  const float* q_weight;   // [d_q, d_z]
+  const float* leaf_V;     // [d_z, r_leaf]
+  const float* leaf_U;     // [r_leaf, d_m]
+  const float* leaf_h;     // [n, r_leaf]
+  const float* merge_T;    // [d_m / 32, 32, 32, 32]
+  const float* merge_V;    // [d_m, r_merge]
+  const float* merge_U;    // [r_merge, d_m]
+  const float* merge_h;    // [levels, n / 2, r_merge]
+  const uint8_t* opcodes;  // [levels, n / 2]
+  const float* readout_V;  // [d_m, r_out]
+  const float* readout_U;  // [r_out, 2]
+  const float* readout_h;  // [r_out]
+  float* log_abs;          // [B]
+  float* phase;            // [B]
+  float* workspace;
+  int64_t B;
+  int n, d_q, d_z, r_leaf, d_m, r_merge, r_out;
+  float merge_eps;
+};
+constexpr int kRowMaxFloats = 2048;  // widest carrier row the row epilogues take
+int64_t compiled_wavefunction_workspace_bytes(int64_t B, int64_t n, int64_t d_z, int64_t r_leaf, int64_t d_m,
+                                              int64_t r_merge, int64_t r_out);
+hipError_t launch_compiled_wavefunction(const WaveFnParams& p, hipStream_t stream);
 constexpr int64_t kApplyScratchFloats = int64_t(8) << 20;           // 32 MiB
 constexpr int64_t kApplyScratchMaxRank = kApplyScratchFloats / 128;  // 65536
 hipError_t launch_factorized_apply_noalloc(const float* x, const float* V, const float* h, const float* U,

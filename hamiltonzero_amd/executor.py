@@ -87,3 +87,77 @@ def _factorized_apply(factor, h: Tensor, x: Tensor, residual: Optional[Tensor] =
 
 
 factorized_apply = _factorized_apply
+
+
+def _single(values, name: str):
+    """Exactly one entry (``compiled/execute.py:16-21``)."""
+    if len(values) != 1:
+        raise ValueError(f"compiled HT executor requires exactly one {name}; got {len(values)}")
+    return values[0]
+
+
+def execute_wavefunction(kernel, tree, q_routed: Tensor) -> tuple[Tensor, Tensor]:
+    """(log|psi|, phase) of every walker (``compiled/execute.py:79-125``), all on the GPU in
+    one ``hz_compiled_wavefunction`` call.
+
+    ``kernel`` and ``tree`` have the reference's structure (``compiled/types.py``):
+    ``kernel.q_to_odd.weight``, ``kernel.leaf_factors`` / ``merge_factors`` /
+    ``readout_factors`` (one factor each, with ``V`` and ``U``), ``kernel.merge_T``,
+    ``kernel.merge_eps``; ``tree.leaf_h``, ``tree.readout_h`` (one entry each),
+    ``tree.merge_h`` and ``tree.opcodes`` (one entry per level). ``q_routed`` is
+    ``[..., n_sites, d_q]``. The structure checks raise the reference's errors."""
+    if len(getattr(tree, "leaf_combiner_h", ())) != 0 or len(getattr(tree, "readout_combiner_h", ())) != 0:
+        raise ValueError("single-head compiled HT executor does not accept combiners")
+    if len(tree.merge_h) != len(tree.opcodes):
+        raise ValueError("merge_h and opcodes must have one entry per tree level")
+    leaf = _single(kernel.leaf_factors, "leaf factor")
+    merge = _single(kernel.merge_factors, "merge factor")
+    readout = _single(kernel.readout_factors, "readout factor")
+    leaf_h = _single(tree.leaf_h, "leaf conditioner")
+    readout_h = _single(tree.readout_h, "readout conditioner").reshape(-1)
+    n = q_routed.shape[-2]
+    width = n
+    for h_level in tree.merge_h:
+        if width != 2 * h_level.shape[-2]:
+            raise ValueError("compiled merge level has incompatible shrinking shape")
+        width //= 2
+    if width != 1:
+        raise ValueError("compiled tree did not reduce to one root")
+    dev = q_routed.device
+    q_weight = kernel.q_to_odd.weight
+    T = kernel.merge_T
+    G, d_r = T.shape[0], T.shape[1]
+    d_q, d_z = q_weight.shape
+    R_leaf, d_m = leaf.U.shape
+    R_merge = merge.V.shape[1]
+    R_out = readout.V.shape[1]
+    lead = q_routed.shape[:-2]
+    B = 1
+    for s in lead:
+        B *= s
+    ops = [_check("q_routed", q_routed.reshape(B, n, d_q), dev), _check("q_to_odd.weight", q_weight, dev),
+           _check("leaf V", leaf.V, dev), _check("leaf U", leaf.U, dev), _check("leaf_h", leaf_h, dev),
+           _check("merge_T", T, dev), _check("merge V", merge.V, dev), _check("merge U", merge.U, dev)]
+    levels = len(tree.merge_h)
+    half = max(n // 2, 1)
+    # the reference's packed per-level storage (compiled/model.py:58-90): rows past a level's
+    # width are zero conditioners with EMPTY opcodes
+    merge_h = torch.zeros((max(levels, 1), half, R_merge), dtype=torch.float32, device=dev)
+    opcodes = torch.full((max(levels, 1), half), 3, dtype=torch.uint8, device=dev)
+    for level, (h_level, op_level) in enumerate(zip(tree.merge_h, tree.opcodes)):
+        w = h_level.shape[-2]
+        merge_h[level, :w] = _check("merge_h", h_level, dev)
+        opcodes[level, :w] = op_level.to(device=dev, dtype=torch.uint8)
+    ops += [merge_h, opcodes, _check("readout V", readout.V, dev), _check("readout U", readout.U, dev),
+            _check("readout_h", readout_h, dev)]
+    log_abs = torch.empty(B, dtype=torch.float32, device=dev)
+    phase = torch.empty(B, dtype=torch.float32, device=dev)
+    lib = _native.lib()
+    nbytes = lib.hz_compiled_wavefunction_workspace(B, n, d_z, R_leaf, d_m, R_merge, R_out)
+    if nbytes < 0:
+        raise ValueError("every size of the compiled wavefunction must be >= 1")
+    work = torch.empty(nbytes // 4 + 64, dtype=torch.float32, device=dev)
+    _native.check(lib.hz_compiled_wavefunction(
+        torch.cuda.current_stream(dev).cuda_stream, *(_ptr(t) for t in ops), _ptr(log_abs), _ptr(phase), _ptr(work),
+        nbytes, B, n, d_q, d_z, R_leaf, G, d_r, R_merge, R_out, float(kernel.merge_eps)))
+    return log_abs.reshape(lead), phase.reshape(lead)

@@ -250,3 +250,47 @@ def time_trunk_walkers_per_s(inputs: dict, mask, params: dict, gain: float, d_he
             break
     return {"walkers_per_s": prim[0].shape[0] * reps / el, "seconds": el, "reps": reps, "threads": threads,
             "cpu_model": host_cpu_model(), "host_cpus": host_cpus(), "y": y.detach(), "ty": ty.detach()}
+
+
+def compiled_wavefunction(p: dict, merge_eps: float):
+    """CompiledFinetuneWaveFunction._forward_plain (compiled/model.py:143-180) in torch-CPU
+    float32 on a dict of packed parameters (merge_h [L, n/2, R], opcodes [L, n/2])."""
+    q = p["q"]
+    B, n = q.shape[0], q.shape[1]
+    z = q @ p["q_weight"]
+    u = ((z @ p["leaf_V"]) * p["leaf_h"]) @ p["leaf_U"]
+    rms = torch.sqrt(torch.mean(u * u, dim=-1, keepdim=True) + 1e-30)
+    u, s = u / rms, torch.log(rms)[..., 0]
+    level, width = 0, n // 2
+    G, R = p["merge_T"].shape[0], p["merge_T"].shape[1]
+    while width >= 1:
+        ul, ur, sl, sr = u[:, 0::2], u[:, 1::2], s[:, 0::2], s[:, 1::2]
+        raw = torch.einsum("ijkl,Bik,Bil->Bij", p["merge_T"], ul.reshape(-1, G, R), ur.reshape(-1, G, R))
+        raw = raw.reshape(B, width, G * R)
+        out = raw + ((raw @ p["merge_V"]) * p["merge_h"][level, :width]) @ p["merge_U"]
+        scale = torch.sqrt(torch.mean(out * out, dim=-1) + merge_eps)
+        ops = p["opcodes"][level, :width]
+        both, left, right = ((ops == c).to(u.dtype) for c in (0, 1, 2))
+        u = both[:, None] * (out / scale[..., None]) + left[:, None] * ul + right[:, None] * ur
+        s = both * (sl + sr + torch.log(scale)) + left * sl + right * sr
+        level, width = level + 1, width // 2
+    psi = ((u[:, 0] @ p["readout_V"]) * p["readout_h"]) @ p["readout_U"]
+    return 0.5 * torch.log(psi[:, 0] ** 2 + psi[:, 1] ** 2) + s[:, 0], torch.atan2(psi[:, 1], psi[:, 0])
+
+
+def time_wavefunction_walkers_per_s(p: dict, merge_eps: float, budget_s: float = 15.0,
+                                    threads: int | None = None) -> dict:
+    """Time :func:`compiled_wavefunction` on the walkers of ``p['q']``."""
+    threads = threads or default_threads()
+    torch.set_num_threads(threads)
+    with torch.no_grad():
+        la, ph = compiled_wavefunction(p, merge_eps)
+        reps, t0 = 0, time.perf_counter()
+        while True:
+            la, ph = compiled_wavefunction(p, merge_eps)
+            reps += 1
+            el = time.perf_counter() - t0
+            if el >= budget_s or reps >= 100000:
+                break
+    return {"walkers_per_s": p["q"].shape[0] * reps / el, "seconds": el, "reps": reps, "threads": threads,
+            "cpu_model": host_cpu_model(), "host_cpus": host_cpus(), "log_abs": la, "phase": ph}

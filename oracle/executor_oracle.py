@@ -15,11 +15,21 @@ at every tree level (paths relative to ``src/hamiltonzero/``):
   way the executor passes it (one row of h per tree node).
 * ``merge_level`` — one level of ``execute_wavefunction`` (``compiled/execute.py:98-113``):
   the merge, its residual factorized apply, the RMS rescale and the opcode gate.
+* ``normalize_leaf_carriers`` — ``model/model.py:31-37``.
+* ``execute_wavefunction`` — the whole per-walker forward
+  (``CompiledFinetuneWaveFunction._forward_plain``, ``compiled/model.py:143-180``): leaf,
+  every level, readout, (log|psi|, phase).
+* ``classify_opcodes`` — the opcodes of a tree over a leaf_real mask
+  (``compiled/tree.py:344-360``): MERGE where both children hold a real leaf, CARRY_LEFT /
+  CARRY_RIGHT where one does, EMPTY where neither.
 
 How each function is pinned (tests/test_executor_oracle.py): explicit Python loops on tiny
 inputs, closed forms (a T that copies one operand, the identity factors), bilinearity and
 the (k, l) exchange symmetry of the merge, linearity and the conditioner scaling of the
-apply. No function here is "parity unpinned".
+apply; for the whole wavefunction, trees of carries only (the root is then the first or the
+last leaf, whose log|psi| needs no merge at all), the homogeneity of a tree of merges
+(scaling q_to_odd by a adds n log a to log|psi| and leaves the phase), an EMPTY root
+(psi = 0) and planted mistakes. No function here is "parity unpinned".
 """
 
 from __future__ import annotations
@@ -68,6 +78,44 @@ def merge_level(T, V, U, h_level, eps, u, s, opcodes):
     u_new = both[:, None] * cand_u + left[:, None] * u_left + right[:, None] * u_right
     s_new = both * cand_s + left * s_left + right * s_right
     return u_new, s_new
+
+
+def normalize_leaf_carriers(u):
+    """(u / rms, log rms) with rms = sqrt(mean(u^2) + 1e-30) over the last axis
+    (model/model.py:31-37)."""
+    u = _f64(u)
+    rms = np.sqrt(np.mean(u * u, axis=-1, keepdims=True) + 1e-30)
+    return u / rms, np.log(rms)[..., 0]
+
+
+def execute_wavefunction(q, q_weight, leaf_V, leaf_U, leaf_h, merge_T, merge_V, merge_U, merge_h, opcodes,
+                         readout_V, readout_U, readout_h, merge_eps):
+    """(log|psi|, phase) per walker (compiled/model.py:143-180). q [..., n, d_q]; merge_h and
+    opcodes are per-level sequences ([w, R_merge], [w]) for widths n/2, ..., 1."""
+    z = _f64(q) @ _f64(q_weight)
+    u, s = normalize_leaf_carriers(factorized_apply(leaf_V, leaf_U, leaf_h, z))
+    for h_level, ops in zip(merge_h, opcodes):
+        u, s = merge_level(merge_T, merge_V, merge_U, h_level, merge_eps, u, s, ops)
+    psi = factorized_apply(readout_V, readout_U, readout_h, u[..., 0, :])
+    re, im = psi[..., 0], psi[..., 1]
+    with np.errstate(divide="ignore"):
+        log_abs = 0.5 * np.log(re * re + im * im) + s[..., 0]
+    return log_abs, np.arctan2(im, re)
+
+
+def classify_opcodes(leaf_real):
+    """Per-level opcodes of the pairwise tree over a [n] leaf_real mask (compiled/tree.py:344-360)."""
+    real = np.asarray(leaf_real, dtype=bool)
+    levels = []
+    while real.shape[0] > 1:
+        left, right = real[0::2], real[1::2]
+        ops = np.full(left.shape, EMPTY, dtype=np.uint8)
+        ops[left & right] = MERGE
+        ops[left & ~right] = CARRY_LEFT
+        ops[~left & right] = CARRY_RIGHT
+        levels.append(ops)
+        real = left | right
+    return levels
 
 
 def loop_quadrilinear_merge(T, u_a, u_b):

@@ -14,7 +14,7 @@ HEADERS = sorted((Path(__file__).resolve().parents[1] / "include").glob("*.h"))
 
 def header_functions():
     text = "\n".join(h.read_text() for h in HEADERS)
-    return sorted(set(re.findall(r"^\s*(?:int|const char\*)\s+(hz_\w+)\s*\(", text, flags=re.M)))
+    return sorted(set(re.findall(r"^\s*(?:int|int64_t|const char\*)\s+(hz_\w+)\s*\(", text, flags=re.M)))
 
 
 @pytest.fixture(scope="module")
@@ -201,3 +201,36 @@ def test_noalloc_apply_rejects_bad_arguments(lib):
     assert na(None, A, A, A, A, None, A, 0, 1536, 1024, 1536, 32) == _native.HZ_EINVAL
     assert na(None, A, A, A, A, None, None, 64, 1536, 1024, 1536, 32) == _native.HZ_ENULL
     assert na(None, A, A, A, A, A + 8, A, 64, 1536, 1024, 1536, 32) == _native.HZ_EALIGN
+
+
+def test_compiled_wavefunction_rejects_bad_arguments(lib):
+    ws = lib.hz_compiled_wavefunction_workspace
+    need = ws(4, 8, 32, 64, 64, 32, 16)
+    assert need > 0 and ws(0, 8, 32, 64, 64, 32, 16) == -1
+    f = lib.hz_compiled_wavefunction
+    assert len(f.argtypes) == 28
+    names = ["stream", "q", "q_weight", "leaf_V", "leaf_U", "leaf_h", "merge_T", "merge_V", "merge_U", "merge_h",
+             "opcodes", "readout_V", "readout_U", "readout_h", "log_abs", "phase", "workspace", "workspace_bytes",
+             "B", "n_sites", "d_q", "d_z", "R_leaf", "G", "d_r", "R_merge", "R_out", "merge_eps"]
+    base = [None] + [A] * 16 + [need, 4, 8, 4, 32, 64, 2, 32, 32, 16, 1e-6]
+
+    def call(**over):
+        args = list(base)
+        for key, val in over.items():
+            args[names.index(key)] = val
+        return f(*args)
+
+    cases = [
+        (dict(n_sites=6), _native.HZ_EINVAL, "power of two"),
+        (dict(d_r=16), _native.HZ_EINVAL, "rank must be 32"),
+        (dict(G=65), _native.HZ_EINVAL, "exceeds 2048"),
+        (dict(B=0), _native.HZ_EINVAL, ">= 1"),
+        (dict(workspace_bytes=need - 4), _native.HZ_EINVAL, "workspace_bytes"),
+        (dict(merge_eps=float("nan")), _native.HZ_EINVAL, "merge_eps"),
+        (dict(q=None), _native.HZ_ENULL, "q must not be NULL"),
+        (dict(opcodes=None), _native.HZ_ENULL, "opcodes"),
+        (dict(leaf_h=A + 4), _native.HZ_EALIGN, "leaf_h"),
+    ]
+    for over, code, needle in cases:
+        assert call(**over) == code, over
+        assert needle in lib.hz_last_error().decode(), over

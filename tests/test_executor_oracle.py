@@ -155,3 +155,107 @@ def test_cpu_baseline_level_matches_oracle():
     raw = X.quadrilinear_merge(T, ul, ur)
     want = raw + X.factorized_apply(V, U, h, raw.reshape(B, W, -1)).reshape(raw.shape)
     assert rel(got, want) < 1e-5
+
+
+def _wavefn_inputs(seed, B=3, n=8, d_q=4, d_z=6, R_leaf=10, G=2, R=4, R_merge=9, R_out=5):
+    rng = np.random.default_rng(seed)
+    dm = G * R
+    w = lambda i, o: rng.standard_normal((i, o)) / np.sqrt(i)  # noqa: E731
+    p = dict(q=rng.standard_normal((B, n, d_q)), q_weight=w(d_q, d_z), leaf_V=w(d_z, R_leaf), leaf_U=w(R_leaf, dm),
+             leaf_h=rng.standard_normal((n, R_leaf)), merge_T=rng.standard_normal((G, R, R, R)) / R,
+             merge_V=w(dm, R_merge), merge_U=w(R_merge, dm), readout_V=w(dm, R_out), readout_U=w(R_out, 2),
+             readout_h=rng.standard_normal(R_out), merge_eps=1e-6)
+    p["merge_h"] = [rng.standard_normal((n >> (l + 1), R_merge)) for l in range(int(np.log2(n)))]
+    return p
+
+
+def _leaf_only(p, leaf):
+    """log|psi| and phase of a tree that carries one leaf to the root: its normalised
+    carrier goes straight to the readout (no merge, no level rescale)."""
+    z = p["q"][:, leaf] @ p["q_weight"]
+    u_raw = ((z @ p["leaf_V"]) * p["leaf_h"][leaf]) @ p["leaf_U"]
+    rms = np.sqrt(np.mean(u_raw ** 2, axis=-1) + 1e-30)
+    psi = ((u_raw / rms[:, None]) @ p["readout_V"] * p["readout_h"]) @ p["readout_U"]
+    return 0.5 * np.log(psi[:, 0] ** 2 + psi[:, 1] ** 2) + np.log(rms), np.arctan2(psi[:, 1], psi[:, 0])
+
+
+@pytest.mark.parametrize("op,leaf", [(X.CARRY_LEFT, 0), (X.CARRY_RIGHT, 7)])
+def test_wavefunction_of_carries_is_one_leaf(op, leaf):
+    p = _wavefn_inputs(30)
+    ops = [np.full(len(h), op, dtype=np.uint8) for h in p["merge_h"]]
+    la, ph = X.execute_wavefunction(opcodes=ops, **p)
+    want_la, want_ph = _leaf_only(p, leaf)
+    assert rel(la, want_la) < 1e-12 and rel(ph, want_ph) < 1e-12
+
+
+def test_wavefunction_of_merges_is_homogeneous_in_the_leaf_scale():
+    """psi is multilinear in the n leaf carriers: q_to_odd scaled by a adds n log a to
+    log|psi| and leaves the phase (every level rescales its carriers)."""
+    p = _wavefn_inputs(31)
+    ops = [np.full(len(h), X.MERGE, dtype=np.uint8) for h in p["merge_h"]]
+    la, ph = X.execute_wavefunction(opcodes=ops, **p)
+    la2, ph2 = X.execute_wavefunction(opcodes=ops, **dict(p, q_weight=2.5 * p["q_weight"]))
+    assert np.allclose(la2 - la, 8 * np.log(2.5), atol=1e-10)
+    assert np.allclose(ph2, ph, atol=1e-10)
+
+
+def test_wavefunction_composes_the_pinned_pieces():
+    p = _wavefn_inputs(32, n=4)
+    ops = X.classify_opcodes([True, False, True, True])
+    assert [o.tolist() for o in ops] == [[X.CARRY_LEFT, X.MERGE], [X.MERGE]]
+    la, ph = X.execute_wavefunction(opcodes=ops, **p)
+    B, n = p["q"].shape[:2]
+    z = (p["q"] @ p["q_weight"]).reshape(B * n, -1)
+    u_raw = X.loop_factorized_apply(p["leaf_V"], p["leaf_U"], np.tile(p["leaf_h"], (B, 1)), z).reshape(B, n, -1)
+    u, s = X.normalize_leaf_carriers(u_raw)
+    for h, o in zip(p["merge_h"], ops):
+        u, s = X.merge_level(p["merge_T"], p["merge_V"], p["merge_U"], h, p["merge_eps"], u, s, o)
+    psi = X.loop_factorized_apply(p["readout_V"], p["readout_U"], np.tile(p["readout_h"], (B, 1)), u[:, 0])
+    assert rel(la, 0.5 * np.log(psi[:, 0] ** 2 + psi[:, 1] ** 2) + s[:, 0]) < 1e-12
+    assert rel(ph, np.arctan2(psi[:, 1], psi[:, 0])) < 1e-12
+
+
+def test_wavefunction_empty_root_and_leaf_normalisation():
+    p = _wavefn_inputs(33, n=2)
+    la, ph = X.execute_wavefunction(opcodes=[np.array([X.EMPTY], np.uint8)], **p)
+    assert np.all(np.isneginf(la)) and np.all(ph == 0.0)
+    u, s = X.normalize_leaf_carriers(np.array([[3.0, 4.0]]))
+    assert np.allclose(u, [[3 / np.sqrt(12.5), 4 / np.sqrt(12.5)]]) and np.allclose(s, 0.5 * np.log(12.5))
+
+
+def test_planted_swapped_carry_is_caught(monkeypatch):
+    p = _wavefn_inputs(34)
+    ops = [np.full(len(h), X.CARRY_LEFT, dtype=np.uint8) for h in p["merge_h"]]
+    real = X.merge_level
+
+    def swapped(T, V, U, h, eps, u, s, o):
+        o = np.where(o == X.CARRY_LEFT, X.CARRY_RIGHT, np.where(o == X.CARRY_RIGHT, X.CARRY_LEFT, o))
+        return real(T, V, U, h, eps, u, s, o)
+
+    monkeypatch.setattr(X, "merge_level", swapped)
+    la, _ = X.execute_wavefunction(opcodes=ops, **p)
+    want, _ = _leaf_only(p, 0)
+    assert rel(la, want) > 1e-3
+
+
+def test_cpu_baseline_wavefunction_matches_oracle():
+    """bench.py's CPU leg for the wavefunction (torch-CPU float32, packed per-level storage)
+    agrees with the float64 oracle."""
+    import torch
+
+    from oracle import cpu_baseline
+
+    p = _wavefn_inputs(35, B=3, n=8, G=2, R=32)
+    ops = X.classify_opcodes([True, True, False, True, True, True, True, False])
+    la, ph = X.execute_wavefunction(opcodes=ops, **p)
+    L, half, Rm = len(p["merge_h"]), 4, p["merge_h"][0].shape[1]
+    mh = np.zeros((L, half, Rm))
+    oc = np.full((L, half), X.EMPTY, np.uint8)
+    for lv, (h, o) in enumerate(zip(p["merge_h"], ops)):
+        mh[lv, : len(h)], oc[lv, : len(o)] = h, o
+    t = lambda x: torch.from_numpy(np.asarray(x, np.float32))  # noqa: E731
+    packed = {k: t(p[k]) for k in ("q", "q_weight", "leaf_V", "leaf_U", "leaf_h", "merge_T", "merge_V", "merge_U",
+                                   "readout_V", "readout_U", "readout_h")}
+    packed["merge_h"], packed["opcodes"] = t(mh), torch.from_numpy(oc)
+    r = cpu_baseline.time_wavefunction_walkers_per_s(packed, p["merge_eps"], budget_s=0.05, threads=2)
+    assert rel(r["log_abs"].numpy(), la) < 1e-4 and rel(r["phase"].numpy(), ph) < 1e-4

@@ -111,3 +111,93 @@ def test_merge_level_products_compose():
     raw_ref = X.quadrilinear_merge(T, ul, ur)
     want = raw_ref + X.factorized_apply(V, U, h, raw_ref)
     assert rel(out.cpu().numpy(), want) <= TOL
+
+
+def _wavefn_case(seed, B, n, d_q, d_z, R_leaf, G, R_merge, R_out, real):
+    rng = np.random.default_rng(seed)
+    R, dm = 32, G * 32
+    f32 = lambda x: np.asarray(x, dtype=np.float32)  # noqa: E731
+    w = lambda i, o: f32(rng.standard_normal((i, o)) / np.sqrt(i))  # noqa: E731
+    if real == "all":
+        leaf_real = np.ones(n, bool)
+    else:
+        leaf_real = rng.random(n) < (0.8 if real == "random" else 0.3)
+        leaf_real[rng.integers(n)] = True
+    p = dict(q=f32(rng.standard_normal((B, n, d_q))), q_weight=w(d_q, d_z), leaf_V=w(d_z, R_leaf),
+             leaf_U=w(R_leaf, dm), leaf_h=f32(rng.standard_normal((n, R_leaf))),
+             merge_T=f32(rng.standard_normal((G, R, R, R)) / R), merge_V=w(dm, R_merge), merge_U=w(R_merge, dm),
+             readout_V=w(dm, R_out), readout_U=w(R_out, 2), readout_h=f32(rng.standard_normal(R_out)),
+             merge_eps=1e-6)
+    p["merge_h"] = [f32(rng.standard_normal((n >> (l + 1), R_merge))) for l in range(int(np.log2(n)))]
+    p["opcodes"] = X.classify_opcodes(leaf_real) if n > 1 else []
+    return p
+
+
+def _readout_condition(p):
+    """kappa_b = sum_r |m_r| (|U_r0| + |U_r1|) / |psi_b| from the oracle's root carriers."""
+    z = np.asarray(p["q"], np.float64) @ p["q_weight"]
+    u, s = X.normalize_leaf_carriers(X.factorized_apply(p["leaf_V"], p["leaf_U"], p["leaf_h"], z))
+    for h, o in zip(p["merge_h"], p["opcodes"]):
+        u, s = X.merge_level(p["merge_T"], p["merge_V"], p["merge_U"], h, p["merge_eps"], u, s, o)
+    m = (u[:, 0] @ np.asarray(p["readout_V"], np.float64)) * p["readout_h"]
+    U = np.asarray(p["readout_U"], np.float64)
+    psi = m @ U
+    return (np.abs(m) @ np.abs(U)).sum(axis=1) / np.hypot(psi[:, 0], psi[:, 1])
+
+
+def _namespaces(p):
+    t = lambda x: torch.from_numpy(np.ascontiguousarray(x)).cuda()  # noqa: E731
+    fac = lambda V, U: types.SimpleNamespace(V=t(V), U=t(U))  # noqa: E731
+    kernel = types.SimpleNamespace(q_to_odd=types.SimpleNamespace(weight=t(p["q_weight"])),
+                                   leaf_factors=(fac(p["leaf_V"], p["leaf_U"]),), merge_T=t(p["merge_T"]),
+                                   merge_factors=(fac(p["merge_V"], p["merge_U"]),),
+                                   readout_factors=(fac(p["readout_V"], p["readout_U"]),), merge_eps=p["merge_eps"])
+    tree = types.SimpleNamespace(leaf_h=(t(p["leaf_h"]),), readout_h=(t(p["readout_h"]),), leaf_combiner_h=(),
+                                 readout_combiner_h=(), merge_h=tuple(t(h) for h in p["merge_h"]),
+                                 opcodes=tuple(t(o) for o in p["opcodes"]))
+    return kernel, tree, t(p["q"])
+
+
+@pytest.mark.parametrize(
+    "B,n,d_q,d_z,R_leaf,G,R_merge,R_out,real",
+    [
+        (16, 64, 4, 32, 1536, 48, 1024, 64, "random"),  # the fine-tune sizes (config.py:21-29,189-190)
+        (5, 8, 4, 40, 24, 4, 96, 8, "all"),
+        (7, 16, 3, 30, 66, 2, 50, 6, "sparse"),          # sizes off the 4-float staging path
+        (3, 1, 4, 32, 64, 3, 32, 16, "all"),             # one site: no merge level
+        (300, 4, 4, 32, 128, 8, 64, 64, "random"),       # many walkers, shallow tree
+    ],
+)
+def test_compiled_wavefunction_matches_oracle(B, n, d_q, d_z, R_leaf, G, R_merge, R_out, real):
+    from hamiltonzero_amd import executor
+
+    _say(f"wavefunction B={B} n={n} G={G} R_leaf={R_leaf} R_merge={R_merge} R_out={R_out} {real}")
+    p = _wavefn_case(B * 3 + n, B, n, d_q, d_z, R_leaf, G, R_merge, R_out, real)
+    kernel, tree, q = _namespaces(p)
+    la, ph = executor.execute_wavefunction(kernel, tree, q)
+    torch.cuda.synchronize()
+    want_la, want_ph = X.execute_wavefunction(**p)
+    # log|psi| and the phase carry psi's relative error. Where the readout's sum cancels,
+    # kappa = sum_r |m_r| (|U_r0| + |U_r1|) / |psi| (m the conditioned readout row), that is
+    # kappa times the float32 error of its terms (about 2e-7 kappa measured), so each walker
+    # is allowed 1e-6 kappa on top of the max-norm bound.
+    kappa = _readout_condition(p)
+    dla = np.abs(la.cpu().numpy().astype(np.float64) - want_la)
+    assert np.all(dla <= TOL * np.max(np.abs(want_la)) + 1e-6 * kappa), (dla.max(), kappa[np.argmax(dla)])
+    dphi = np.abs(np.angle(np.exp(1j * (ph.cpu().numpy().astype(np.float64) - want_ph))))
+    assert np.all(dphi <= TOL * np.pi + 1e-6 * kappa), (dphi.max(), kappa[np.argmax(dphi)])
+    assert np.median(kappa) < 10  # most walkers are well conditioned: the bound is mostly the max-norm one
+
+
+def test_compiled_wavefunction_structure_errors():
+    from hamiltonzero_amd import executor
+
+    _say("wavefunction structure errors")
+    p = _wavefn_case(1, 2, 8, 4, 32, 64, 2, 32, 8, "all")
+    kernel, tree, q = _namespaces(p)
+    with pytest.raises(ValueError, match="one entry per tree level"):
+        executor.execute_wavefunction(kernel, types.SimpleNamespace(**dict(vars(tree), opcodes=tree.opcodes[:-1])), q)
+    with pytest.raises(ValueError, match="incompatible shrinking shape"):
+        executor.execute_wavefunction(kernel, tree, q[:, :4])
+    with pytest.raises(ValueError, match="does not accept combiners"):
+        executor.execute_wavefunction(kernel, types.SimpleNamespace(**dict(vars(tree), leaf_combiner_h=(1,))), q)
