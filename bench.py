@@ -41,8 +41,8 @@ RECT_METRIC = "rectangular large-N forward (noncausal_bias_mha) query rows/sec; 
 EXECUTOR_METRIC = "compiled-executor merge level (quadrilinear merge + factorized apply) walkers/sec; % of MFMA roofline"
 WAVEFN_METRIC = ("compiled per-walker wavefunction (leaf, 6 merge levels, readout -> log|psi|, phase) walkers/sec at "
                  "B=1024, 64 sites, fine-tune ranks; % of MFMA roofline")
-TRUNK_METRIC = ("trunk attention with its learned pair bias (ln_edge + bias_mlp producer, then fwd+JVP with the gate "
-                "collapse), walkers/sec at B=1024,L=64; % of MFMA roofline")
+TRUNK_METRIC = ("trunk attention block after W_QKV (ln_edge + bias_mlp producer, fwd+JVP with the gate collapse, "
+                "W_O), walkers/sec at B=1024,L=64; % of MFMA roofline")
 HBM_PEAK_GBS = 8000.0
 FP32_PEAK_TFLOPS = 157.3
 BF16_PEAK_TFLOPS = 2516.6
@@ -116,9 +116,9 @@ CONFIGS = {
     # from the edge features (ln_edge + bias_mlp, trunk.py:89-105; edge_channels 96,
     # bias hidden 64, config.py:28,31) and its tangent, then the gated fwd + JVP.
     "trunk": Config("trunk", 1024, 64, 32, 16, 36, 1, "f32", 7,
-                    "the trunk's attention with its pair bias: edge [1024,64,64,96] and its tangent -> "
+                    "the trunk's attention block after W_QKV: edge [1024,64,64,96] and its tangent -> "
                     "ln_edge + bias_mlp -> e, e_t [1024,64,32,64] -> gated fwd+JVP [1024,64,32,16] -> y, ydot "
-                    "[1024,64,16,16], 36/64 physical sites", cpu_sample=4, metric=TRUNK_METRIC),
+                    "[1024,64,256] -> W_O [256,512] -> delta, delta_t [1024,64,512], 36/64 physical sites", cpu_sample=4, metric=TRUNK_METRIC),
     # The large-N evaluation forward (noncausal_bias_mha via pallas_rectangular_edge_attention):
     # one system, all queries against all keys, dense [Nq, Nk, H] bias.
     "rect": Config("rect", 1, 4096, 16, 64, 4000, 0, "f32", 5,
@@ -598,6 +598,10 @@ def run_trunk(args, cfg):
     d = {"q": rnd(shape, D ** -0.5), "k": rnd(shape, D ** -0.5), "v": rnd(shape),
          "qt": rnd((1, *shape)), "kt": rnd((1, *shape)), "vt": rnd((1, *shape)),
          "edge": rnd((B, N, N, C)), "edge_t": rnd((B, N, N, C))}
+    d_attn, d_e = H // 2 * D, 512  # W_O: attn_dim 256 -> d_e 512 (config.py:17,26; trunk.py:54)
+    w_o = rnd((d_attn, d_e), d_attn ** -0.5)
+    d["delta"] = torch.empty((B, N, d_e), dtype=torch.float32, device=dev)
+    d["delta_t"] = torch.empty((1, B, N, d_e), dtype=torch.float32, device=dev)
     params = {"ln_w": 1.0 + 0.1 * rnd((C,)), "w_in": rnd((C, HID), C ** -0.5), "b_in": rnd((HID,), 0.1),
               "w_1": rnd((HID, HID), HID ** -0.5), "b_1": rnd((HID,), 0.1), "w_2": rnd((HID, HID), HID ** -0.5),
               "b_2": rnd((HID,), 0.1), "w_out": rnd((HID, H), HID ** -0.5), "b_out": rnd((H,), 0.1)}
@@ -622,13 +626,19 @@ def run_trunk(args, cfg):
                                                  P(d["kt"]), P(d["et"]), P(d["vt"]), 1, P(d["y"]), P(d["ty"]), B, N,
                                                  H, D, 1.0, 0))
 
+    def project(i):
+        _native.check(lib.hz_gated_out_proj(s, P(d["y"]), P(d["ty"]), P(w_o), None, P(d["delta"]), P(d["delta_t"]),
+                                            B, N, d_attn, d_e, 1))
+
     def step(i):
         produce(i)
         attend(i)
+        project(i)
 
     ms = timed(step, args.steps, args.warmup, stream)
     ms_prod = timed(produce, args.steps, args.warmup, stream)
     ms_att = timed(attend, args.steps, args.warmup, stream)
+    ms_proj = timed(project, args.steps, args.warmup, stream)
     # The producer's algorithmic work on the pairs it computes (both sites physical): the
     # MLP's products for the primal and the tangent, edge and edge_t rows in, e and e_t out.
     pairs_eff = B * n_phys * n_phys
@@ -647,7 +657,7 @@ def run_trunk(args, cfg):
     roof["reference_equivalent"] = {
         "basis": "every pair computed, as the reference's bias_mlp over the full [N, N] edge tensor does",
         "flops": flops_all, "tflops": flops_all / (ms_prod / 1e3) / 1e12}
-    roof["step"] = {"ms": ms, "producer_ms": ms_prod, "attention_ms": ms_att}
+    roof["step"] = {"ms": ms, "producer_ms": ms_prod, "attention_ms": ms_att, "out_proj_ms": ms_proj}
 
     cpu = None
     if not args.no_cpu_baseline:
@@ -658,14 +668,14 @@ def run_trunk(args, cfg):
                 for nm, t in d.items() if nm in ("q", "k", "v", "qt", "kt", "vt", "edge", "edge_t")}
         hp = {nm: t.cpu() for nm, t in params.items()}
         r = cpu_baseline.time_trunk_walkers_per_s(host, mask[:n].bool().cpu(), hp, gain, D,
-                                                  budget_s=args.cpu_budget)
-        errs = {"y": rel_err(d["y"][:n].cpu().numpy(), r["y"].numpy()),
-                "ty": rel_err(d["ty"][0, :n].cpu().numpy(), r["ty"].numpy())}
+                                                  budget_s=args.cpu_budget, w_o=w_o.cpu())
+        errs = {"delta": rel_err(d["delta"][:n].cpu().numpy(), r["y"].numpy()),
+                "delta_t": rel_err(d["delta_t"][0, :n].cpu().numpy(), r["ty"].numpy())}
         tol = 2e-5
         cpu = {"value": r["walkers_per_s"], "unit": "walkers/s", "cores": r["threads"], "kind": "port",
                "sample": f"the first {n} walkers of the same inputs, {r['reps']} reps in {r['seconds']:.1f} s, "
                          f"torch-CPU fp32 port of the jnp path (ln_edge + bias_mlp over every pair, then the "
-                         f"attention and gate collapse, forward mode by torch.func.jvp) ({r['cpu_model']})",
+                         f"attention, gate collapse and W_O, forward mode by torch.func.jvp) ({r['cpu_model']})",
                "host_cpus": r["host_cpus"],
                "check": {"max_rel_err_vs_gpu": errs, "tol": tol, "ok": all(v <= tol for v in errs.values())}}
     line = {

@@ -117,11 +117,12 @@ constexpr int kBM = 128, kBN = 128, kBK = 16;
 constexpr int kAPad = kBM + 16;
 constexpr int kBPad = kBN + 16;
 
-enum GemmEpi { kEpiPlain = 0, kEpiCond = 1, kEpiResidual = 2 };
+enum GemmEpi { kEpiPlain = 0, kEpiCond = 1, kEpiResidual = 2, kEpiRowMask = 3 };
 
 // C[M, N] = A[M, K] B[K, N] (row-major); EPI: kEpiCond multiplies C[m, n] by
 // h[((row0 + m) mod h_rows) * N + n] (row0: the first row's index in the caller's full
-// row range, nonzero when the rows are processed in chunks); kEpiResidual adds res[m, n].
+// row range, nonzero when the rows are processed in chunks); kEpiResidual adds res[m, n];
+// kEpiRowMask multiplies row m by (mask[m] != 0), aux then being a uint8 mask.
 // C may be the residual itself (each output entry reads its residual entry, then overwrites
 // it, in one thread), so neither carries __restrict__. VEC: K and N are multiples of 4
 // (16-byte staging loads); otherwise the staging loads are per element.
@@ -227,6 +228,7 @@ gemm_f32_kernel(const float* __restrict__ A, const float* __restrict__ Bm, float
         float v = acc[mt][nt][r];
         if constexpr (EPI == kEpiCond) v *= aux[((row0 + row) % h_rows) * N + col];
         if constexpr (EPI == kEpiResidual) v += aux[row * N + col];
+        if constexpr (EPI == kEpiRowMask) v *= reinterpret_cast<const uint8_t*>(aux)[row] != 0 ? 1.f : 0.f;
         C[row * N + col] = v;
       }
     }
@@ -446,6 +448,13 @@ hipError_t launch_factorized_apply(const float* x, const float* V, const float* 
                                    const float* residual, float* y, float* work, int64_t M, int d_in, int R, int d_out,
                                    int h_rows, hipStream_t stream) {
   return apply_rows(x, V, h, U, residual, y, work, M, d_in, R, d_out, h_rows, 0, stream);
+}
+
+hipError_t launch_out_proj(const float* y, const float* w_o, const uint8_t* mask, float* delta, int64_t M, int d_in,
+                           int d_out, hipStream_t stream) {
+  if (mask != nullptr)
+    return launch_gemm<kEpiRowMask>(y, w_o, delta, reinterpret_cast<const float*>(mask), M, d_out, d_in, 1, 0, stream);
+  return launch_gemm<kEpiPlain>(y, w_o, delta, nullptr, M, d_out, d_in, 1, 0, stream);
 }
 
 static hipError_t apply_scratch_address(int device, float** ptr) {

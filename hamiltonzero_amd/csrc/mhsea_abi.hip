@@ -560,4 +560,29 @@ int hz_compiled_wavefunction(hipStream_t stream, const float* q, const float* q_
   return launched(hz::launch_compiled_wavefunction(p, stream));
 }
 
+int hz_gated_out_proj(hipStream_t stream, const float* y, const float* ty, const float* w_o, const uint8_t* mask,
+                      float* delta, float* delta_t, int64_t B, int64_t N, int64_t d_attn, int64_t d_e, int64_t T) {
+  if (B < 1 || N < 1 || d_attn < 1 || d_e < 1) return fail(HZ_EINVAL, "B, N, d_attn and d_e must be >= 1");
+  if (T < 0 || T > 3) return fail(HZ_EINVAL, "T must be in [0, 3], got %lld", (long long)T);
+  if (d_attn > 0x7fffffffLL || d_e > 0x7fffffffLL) return fail(HZ_EINVAL, "dimensions exceed the 32-bit range");
+  const int64_t M = B * N;
+  if ((M + 127) / 128 > 65535) return fail(HZ_EINVAL, "B * N = %lld exceeds the grid limit", (long long)M);
+  HZ_REQUIRE(y);
+  HZ_REQUIRE(w_o);
+  HZ_OPTIONAL(mask);
+  HZ_REQUIRE(delta);
+  if (T > 0) {
+    HZ_REQUIRE(ty);
+    HZ_REQUIRE(delta_t);
+  }
+  if (int rc = launched(hz::launch_out_proj(y, w_o, mask, delta, M, static_cast<int>(d_attn), static_cast<int>(d_e),
+                                            stream)))
+    return rc;
+  for (int64_t t = 0; t < T; ++t)
+    if (int rc = launched(hz::launch_out_proj(ty + t * M * d_attn, w_o, mask, delta_t + t * M * d_e, M,
+                                              static_cast<int>(d_attn), static_cast<int>(d_e), stream)))
+      return rc;
+  return 0;
+}
+
 }  // extern "C"

@@ -116,6 +116,10 @@ hipError_t launch_factorized_apply(const float* x, const float* V, const float* 
 // The same apply with its workspace in a static device array of kApplyScratchFloats floats
 // (executor.hip), rows processed in chunks of whole 128-row tiles; R <= kApplyScratchMaxRank.
 // Allocates nothing.
+// delta = (y W_o) o (mask[row] != 0) over M rows (mask may be null): the attention block's
+// output projection after the gate collapse.
+hipError_t launch_out_proj(const float* y, const float* w_o, const uint8_t* mask, float* delta, int64_t M, int d_in,
+                           int d_out, hipStream_t stream);
 // The whole per-walker wavefunction of the compiled executor (leaf, every merge level,
 // readout) on one stream; workspace of compiled_wavefunction_workspace_bytes().
 struct WaveFnParams {

@@ -277,6 +277,45 @@ def mhsea_fwd_jvp_gated(
     return y, (None if ty is None else (ty if batched else ty[0]))
 
 
+def gated_out_proj(y: Tensor, w_o: Tensor, ty: Optional[Tensor] = None,
+                   mask: Optional[Tensor] = None) -> Tuple[Tensor, Optional[Tensor]]:
+    """The attention block's output projection after the gate collapse: ``delta = y_flat @
+    w_o`` (the trunk's ``W_O``, ``trunk.py:138-144``), times the site mask when ``mask`` is
+    given (the tree's ``mask_q * (out_flat @ w_o)``, ``tree.py:1479-1488``), and the same for
+    each tangent row ``ty [T, ...]`` (or a single ``[...]`` direction). ``y`` is ``[B, N,
+    H/2, D]`` (``mhsea_fwd_jvp_gated``'s output) or ``[B, N, d_attn]``; float32 CUDA tensors."""
+    if y.dim() not in (3, 4):
+        raise ValueError(f"y must be [B, N, H/2, D] or [B, N, d_attn], got {tuple(y.shape)}")
+    B, N = y.shape[0], y.shape[1]
+    d_attn = y[0, 0].numel()
+    if y.dtype != torch.float32 or w_o.dtype != torch.float32:
+        raise TypeError("y and w_o must be float32")
+    if not y.is_cuda:
+        raise ValueError(f"y is on {y.device}: the projection needs GPU tensors")
+    if w_o.dim() != 2 or w_o.shape[0] != d_attn:
+        raise ValueError(f"w_o must be [{d_attn}, d_e], got {tuple(w_o.shape)}")
+    _on_device(y.device, w_o=w_o, ty=ty, mask=mask)
+    d_e = w_o.shape[1]
+    y2, w = y.reshape(B, N, d_attn).contiguous(), w_o.contiguous()
+    batched = ty is not None and ty.dim() == y.dim() + 1
+    t = None if ty is None else (ty if batched else ty.unsqueeze(0))
+    T = 0 if t is None else t.shape[0]
+    if t is not None:
+        if tuple(t.shape[1:]) != tuple(y.shape) or t.dtype != torch.float32:
+            raise ValueError(f"ty must be [T, *{tuple(y.shape)}] float32, got {tuple(ty.shape)} {ty.dtype}")
+        t = t.reshape(T, B, N, d_attn).contiguous()
+    m = None
+    if mask is not None:
+        if tuple(mask.shape) != (B, N):
+            raise ValueError(f"mask must be [B, N] = {(B, N)}, got {tuple(mask.shape)}")
+        m = _mask_u8(mask, y.device)
+    delta = torch.empty((B, N, d_e), dtype=torch.float32, device=y.device)
+    delta_t = torch.empty((T, B, N, d_e), dtype=torch.float32, device=y.device) if T else None
+    _native.check(_native.lib().hz_gated_out_proj(_stream(y.device), _ptr(y2), _ptr(t), _ptr(w), _ptr(m),
+                                                  _ptr(delta), _ptr(delta_t), B, N, d_attn, d_e, T))
+    return delta, (None if delta_t is None else (delta_t if batched else delta_t[0]))
+
+
 def mhsea_bwd(
     q: Tensor,
     k: Tensor,

@@ -161,6 +161,19 @@ int hz_mhsea_fwd_jvp_gated(hipStream_t stream,
                            float scale, int flags);
 
 /*
+ * Output projection of the attention block after the gate collapse, and its tangents.
+ * Replaces the trunk's W_O (src/hamiltonzero/model/trunk.py:138-144) and the tree's w_o with
+ * its site mask (model/tree.py:1479-1488: proposal = mask_q * (out_flat @ w_o)):
+ *     delta[b, i, :]    = (y[b, i, :] W_o) * (mask[b, i] != 0)        (mask NULL: no factor)
+ *     delta_t[t, b, i]  = (ty[t, b, i, :] W_o) * (mask[b, i] != 0)
+ * y [B, N, d_attn] is hz_mhsea_fwd_jvp_gated's y [B, N, H/2, D] read as rows (d_attn =
+ * H/2 * D), ty [T, B, N, d_attn]; W_o [d_attn, d_e] (BiasFreeLinear, [in, out]); float32,
+ * fp32 matrix cores. T in [0, 3].
+ */
+int hz_gated_out_proj(hipStream_t stream, const float* y, const float* ty, const float* w_o, const uint8_t* mask,
+                      float* delta, float* delta_t, int64_t B, int64_t N, int64_t d_attn, int64_t d_e, int64_t T);
+
+/*
  * Reverse mode: cotangents of (q, k, e, v) for the upstream cotangent dout. Replaces the
  * transpose rule _inner_transpose (mhsea_tuned.py:206-221 -> mhsea_backward,
  * custom_gradients.py:78-228 -> mhsea_q_vjp_kernel :231-285, mhsea_kv_vjp_kernel

@@ -223,13 +223,15 @@ def coupling_bias(edge, p, gain, d_head, eps=1e-5):
     return bias.permute(0, 1, 3, 2)
 
 
-def trunk_attention(q, k, v, edge, mask, p, gain, d_head):
-    """The trunk's attention call with its produced bias and the gate collapse (q pre-scaled)."""
-    return gated(q, k, v, mask, coupling_bias(edge, p, gain, d_head))
+def trunk_attention(q, k, v, edge, mask, p, gain, d_head, w_o=None):
+    """The trunk's attention call with its produced bias and the gate collapse (q pre-scaled),
+    then W_O on the flattened heads when given (trunk.py:134-144)."""
+    y = gated(q, k, v, mask, coupling_bias(edge, p, gain, d_head))
+    return y if w_o is None else y.reshape(y.shape[0], y.shape[1], -1) @ w_o
 
 
 def time_trunk_walkers_per_s(inputs: dict, mask, params: dict, gain: float, d_head: int, budget_s: float = 15.0,
-                             threads: int | None = None) -> dict:
+                             threads: int | None = None, w_o=None) -> dict:
     """Time the forward + JVP of :func:`trunk_attention` (tangents on q, k, v and edge) on
     the walkers of ``inputs``; returns walkers/s and the last repetition's y, ydot."""
     threads = threads or default_threads()
@@ -238,7 +240,8 @@ def time_trunk_walkers_per_s(inputs: dict, mask, params: dict, gain: float, d_he
     tans = tuple(inputs[n] for n in ("qt", "kt", "vt", "edge_t"))
 
     def fn():
-        return torch.func.jvp(lambda a, b, c, x: trunk_attention(a, b, c, x, mask, params, gain, d_head), prim, tans)
+        return torch.func.jvp(lambda a, b, c, x: trunk_attention(a, b, c, x, mask, params, gain, d_head, w_o), prim,
+                              tans)
 
     y, ty = fn()  # warm-up
     reps, t0 = 0, time.perf_counter()

@@ -224,6 +224,17 @@ def gated_fwd_jvp(q, k, e, v, mask, qt, kt, et, vt, *, scale=1.0, key_mask=False
     return y, ydot
 
 
+def out_proj(y, w_o, mask=None):
+    """The attention block's output projection after the collapse: ``y_flat @ w_o``
+    (trunk.py:138-144), times ``mask_q`` when a site mask is given (tree.py:1479-1488).
+    y [B, N, H/2, D] or [B, N, d_attn] -> [B, N, d_e]."""
+    y = _f64(y)
+    out = y.reshape(y.shape[0], y.shape[1], -1) @ _f64(w_o)
+    if mask is not None:
+        out = np.asarray(mask, dtype=np.float64)[:, :, None] * out
+    return out
+
+
 def reference_edge_attention(Q, K, V, edge_bias, mask):
     """Per-system jnp op (pallas_attention.py:22-37): [n,h,d], [n,n,h], [n] -> [n,h,d]."""
     d = np.asarray(Q).shape[-1]

@@ -84,3 +84,18 @@ def test_planted_sign_mistake_fails_differences():
     fd = (_y([x[i] + h * tans[i] for i in range(3)], e + h * et, mask)
           - _y([x[i] - h * tans[i] for i in range(3)], e - h * et, mask)) / (2 * h)
     assert rel(wrong, fd) > 1e-3
+
+
+def test_out_proj_matches_loops_and_masks_rows():
+    rng = np.random.default_rng(40)
+    y = rng.standard_normal((2, 3, 2, 4))
+    w = rng.standard_normal((8, 5))
+    mask = np.array([[1, 0, 1], [0, 1, 1]], dtype=bool)
+    got = O.out_proj(y, w, mask)
+    for b in range(2):
+        for i in range(3):
+            flat = [y[b, i, hh, d] for hh in range(2) for d in range(4)]
+            want = [sum(flat[k] * w[k, j] for k in range(8)) * mask[b, i] for j in range(5)]
+            assert np.allclose(got[b, i], want, rtol=1e-13, atol=1e-13)
+    assert np.all(got[~mask] == 0.0)
+    assert np.allclose(O.out_proj(y, w), np.einsum("bihd,hdj->bij", y, w.reshape(2, 4, 5)), rtol=1e-13)

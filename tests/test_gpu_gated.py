@@ -150,3 +150,46 @@ def test_gated_edge_attention_autograd(with_e):
         torch.cuda.synchronize()
         _, want_t = O.gated_fwd_jvp(q, k, e, v, mask, tq[0], tk[0], te[0] if with_e else None, tv[0], scale=scale)
         assert rel(ty.cpu().numpy(), want_t) <= TOL
+
+
+@pytest.mark.parametrize("T,masked,shape", [(0, False, (3, 17, 2, 8, 5)), (1, True, (64, 64, 16, 16, 512)),
+                                            (2, True, (5, 33, 3, 8, 70))])
+def test_gated_out_proj(T, masked, shape):
+    """W_O after the collapse (trunk.py:138-144), with the tree's site mask
+    (tree.py:1479-1488) and the tangents, against the float64 oracle."""
+    from hamiltonzero_amd import kernels
+
+    B, N, hh, D, d_e = shape
+    _say(f"out proj T={T} masked={masked} {shape}")
+    rng = np.random.default_rng(sum(shape) + T)
+    y = rng.standard_normal((B, N, hh, D), dtype=np.float32)
+    ty = rng.standard_normal((max(T, 1), B, N, hh, D), dtype=np.float32)
+    w = (rng.standard_normal((hh * D, d_e)) / np.sqrt(hh * D)).astype(np.float32)
+    mask = rng.random((B, N)) < 0.6 if masked else None
+    dev = lambda x: None if x is None else torch.from_numpy(np.ascontiguousarray(x)).cuda()  # noqa: E731
+    delta, dt = kernels.gated_out_proj(dev(y), dev(w), ty=dev(ty[:T]) if T else None, mask=dev(mask))
+    torch.cuda.synchronize()
+    assert rel(delta.cpu().numpy(), O.out_proj(y, w, mask)) <= TOL
+    if masked:
+        assert np.all(delta.cpu().numpy()[~mask] == 0.0)
+    for t in range(T):
+        assert rel(dt[t].cpu().numpy(), O.out_proj(ty[t], w, mask)) <= TOL
+
+
+def test_gated_then_out_proj_at_the_trunk_shape():
+    """The trunk's attention tail: gated fwd+JVP at [48, 64, 32, 16] with bias, then W_O
+    [256, 512] on y and ydot, against the oracle's chain."""
+    from hamiltonzero_amd import kernels
+
+    _say("gated -> out proj, trunk shape")
+    q, k, v, e, mask, tq, tk, tv, te = make(41, 48, 64, 32, 16, 1, "prefix", True, "qhk")
+    rng = np.random.default_rng(42)
+    w = (rng.standard_normal((256, 512)) / 16.0).astype(np.float32)
+    dev = lambda x: torch.from_numpy(np.ascontiguousarray(x)).cuda()  # noqa: E731
+    y, ty = kernels.mhsea_fwd_jvp_gated(dev(q), dev(k), dev(v), dev(mask), dev(tq[:1]), dev(tk[:1]), dev(tv[:1]),
+                                        e=dev(e), et=dev(te[:1]), scale=0.25)
+    delta, dt = kernels.gated_out_proj(y, dev(w), ty=ty)
+    torch.cuda.synchronize()
+    wy, wty = O.gated_fwd_jvp(q, k, e, v, mask, tq[0], tk[0], te[0], tv[0], scale=0.25)
+    assert rel(delta.cpu().numpy(), O.out_proj(wy, w)) <= TOL
+    assert rel(dt[0].cpu().numpy(), O.out_proj(wty, w)) <= TOL
