@@ -242,15 +242,17 @@ int hz_mhsea_fwd_jvp_gated(hipStream_t stream, const void* q, const void* k, con
   if (int rc = check_dims(B, N, H, D, HZ_DTYPE_F32, flags)) return rc;
   if (T < 0 || T > 2) return fail(HZ_EINVAL, "T must be in [0, 2] for the gated collapse, got %lld", (long long)T);
   if (H % 2 != 0) return fail(HZ_EINVAL, "the gated collapse pairs head h with h + H/2: H must be even, got %lld", (long long)H);
-  if (flags & HZ_FLAG_GENERIC) return fail(HZ_EINVAL, "HZ_FLAG_GENERIC is not available for the gated collapse");
-  // directions per pass: two where the kernel has the T = 2 variant (D <= 16), else one
+  // The producer/consumer kernel where it serves the shape (fp32, N <= 64, D <= 32), in
+  // passes of its tangent variants; otherwise (and with HZ_FLAG_GENERIC) the LDS-streaming
+  // kernel, every direction in one launch.
   auto served = [&](int t) {
-    return hz::pc_fwd_supported(static_cast<int>(N), static_cast<int>(H), static_cast<int>(D), t, HZ_DTYPE_F32);
+    return !(flags & HZ_FLAG_GENERIC) &&
+           hz::pc_fwd_supported(static_cast<int>(N), static_cast<int>(H), static_cast<int>(D), t, HZ_DTYPE_F32);
   };
-  if (!served(T < 1 ? 0 : 1))
-    return fail(HZ_EINVAL, "the gated collapse serves fp32, N <= 64, D in {8, 16, 32}; got N=%lld D=%lld", (long long)N,
-                (long long)D);
-  const int64_t tpass = served(2) ? 2 : 1;
+  const bool use_pc = served(T < 1 ? 0 : 1);
+  // (the LDS-streaming kernel carries the gate terms of two directions in registers below
+  // D = 32; from D = 32 one direction per pass keeps it free of spills)
+  const int64_t tpass = use_pc ? (served(2) ? 2 : 1) : (D >= 32 ? 1 : 2);
   HZ_REQUIRE(q);
   HZ_REQUIRE(k);
   HZ_REQUIRE(v);
@@ -268,8 +270,12 @@ int hz_mhsea_fwd_jvp_gated(hipStream_t stream, const void* q, const void* k, con
   p.lse = nullptr;
   p.gated = 1;
   p.y_tstride = B * N * (H / 2) * D;
+  auto launch = [&](int t) {
+    return use_pc ? hz::launch_fwd_pc(p, static_cast<int>(D), t, false, stream)
+                  : hz::launch_fwd_gated_generic(p, static_cast<int>(D), t, stream);
+  };
   if (T == 0) {
-    if (int rc = launched(hz::launch_fwd_pc(p, static_cast<int>(D), 0, false, stream))) return rc;
+    if (int rc = launched(launch(0))) return rc;
     return keymask_empty_fwd(p, D, 0, false, HZ_DTYPE_F32, stream);
   }
   // Later passes rewrite identical y values, so the call needs no scratch memory.
@@ -284,7 +290,7 @@ int hz_mhsea_fwd_jvp_gated(hipStream_t stream, const void* q, const void* k, con
     p.vt = shift(vt, t0 * ts);
     p.et = shift(et, t0 * es);
     p.tout = static_cast<float*>(ty) + t0 * p.y_tstride;
-    hipError_t err = hz::launch_fwd_pc(p, static_cast<int>(D), static_cast<int>(tn), false, stream);
+    hipError_t err = launch(static_cast<int>(tn));
     if (err != hipSuccess) return launched(err);
   }
   set_tangents(p, ty, qt, kt, et, vt);

@@ -22,6 +22,7 @@
 // The three sums are accumulated with the same online rescaling as out_i, so one pass
 // over the keys produces the primal and all T tangents.
 #include <atomic>
+#include <type_traits>
 
 #include "mhsea_device.h"
 #include "mhsea_launch.h"
@@ -123,8 +124,14 @@ __device__ __forceinline__ void chunk_store(const float4 (&ck)[NPT], const float
 
 // MULTI: N > KC, so keys arrive in several chunks (register prefetch of the next chunk,
 // online rescaling between chunks); otherwise the single chunk holds every key.
-template <int D, int T, bool GIVEN_LSE, bool HAS_E, class S, bool MULTI>
-__global__ void __launch_bounds__(256, (D == 64 && T > 0) ? 2 : 3) mhsea_fwd_kernel(const FwdParams p) {
+// GATED (fp32, no given lse): the grid runs over head pairs; a workgroup computes the gate
+// head h0 and then the value head h0 + H/2 of the same query block in two passes, keeping
+// sigma(g) and sigma'(g) gdot of its rows in registers between them, and writes only the
+// collapse y = sigma(g) v and ydot = sigma'(g) gdot v + sigma(g) vdot ([B, N, H/2, D]).
+template <int D, int T, bool GIVEN_LSE, bool HAS_E, class S, bool MULTI, bool GATED>
+__global__ void __launch_bounds__(256, ((D == 64 && T > 0) || (GATED && D >= 32)) ? 2 : 3)
+    mhsea_fwd_kernel(const FwdParams p) {
+  static_assert(!GATED || (!GIVEN_LSE && std::is_same<S, F32>::value), "the gated collapse is float32, no given lse");
   using Sh = FwdShape<D, T>;
   constexpr int KC = Sh::KC, LD = Sh::LD, DG = Sh::DG, DT = Sh::DT, C4 = Sh::C4, TT = Sh::TT;
   constexpr int NJT = KC / 16;  // 16-key tiles per chunk
@@ -140,12 +147,13 @@ __global__ void __launch_bounds__(256, (D == 64 && T > 0) ? 2 : 3) mhsea_fwd_ker
   int16_t* const idx = reinterpret_cast<int16_t*>(mask_s + n16);
 
   const int N = p.N, H = p.H;
+  const int HG = GATED ? H / 2 : H;  // heads of the grid (head pairs when gated)
   const int nblk = (N + 63) >> 6;
-  const int64_t nwg = static_cast<int64_t>(p.B) * H * nblk;
+  const int64_t nwg = static_cast<int64_t>(p.B) * HG * nblk;
   const int64_t lb = xcd_logical_block(blockIdx.x, nwg);
   const int blk = static_cast<int>(lb % nblk);
-  const int h = static_cast<int>((lb / nblk) % H);
-  const int b = static_cast<int>(lb / (static_cast<int64_t>(nblk) * H));
+  const int h0 = static_cast<int>((lb / nblk) % HG);
+  const int b = static_cast<int>(lb / (static_cast<int64_t>(nblk) * HG));
 
   const int tid = threadIdx.x;
   const int wave = tid >> 6;
@@ -167,11 +175,6 @@ __global__ void __launch_bounds__(256, (D == 64 && T > 0) ? 2 : 3) mhsea_fwd_ker
   const int64_t kts = has_kt ? p.t_stride : 0, vts = has_vt ? p.t_stride : 0;
   const int64_t qts = has_qt ? p.t_stride : 0;
 
-  // ---- issue every global load of the prologue before the first wait ---------------
-  constexpr int NPT = Sh::kPerThread;
-  float4 ck[NPT], cv[NPT], ckt[TT][NPT], cvt[TT][NPT];
-  chunk_load<D, T, S, NPT, TT>(ck, cv, ckt, cvt, p, b, h, 0, nk, key_all, idx, ktp, kts, vtp, vts);
-
   const int q0 = blk * 64 + wave * 16;
   const bool active = q0 < nq;  // wave-uniform
   const bool qvalid = q0 + c < nq;
@@ -179,6 +182,17 @@ __global__ void __launch_bounds__(256, (D == 64 && T > 0) ? 2 : 3) mhsea_fwd_ker
   const int qload = qvalid ? qsite : 0;
   const float qscale = qvalid ? p.scale : 0.f;
   const float qtscale = has_qt ? qscale : 0.f;
+  constexpr int NPT = Sh::kPerThread;
+  float gs[DT][4], gd[TT][DT][4];  // gated: sigma(g), sigma'(g) gdot[t] of this lane's row
+
+#pragma unroll 1
+  for (int pass = 0; pass < (GATED ? 2 : 1); ++pass) {
+  const int h = h0 + pass * HG;  // gated: the gate head, then the value head
+  if (pass > 0) __syncthreads();  // every wave is done with the gate head's last chunk
+
+  // ---- issue every global load of the prologue before the first wait ---------------
+  float4 ck[NPT], cv[NPT], ckt[TT][NPT], cvt[TT][NPT];
+  chunk_load<D, T, S, NPT, TT>(ck, cv, ckt, cvt, p, b, h, 0, nk, key_all, idx, ktp, kts, vtp, vts);
 
   // Query fragment in B-operand layout: lane (g, c) holds q[qsite][g*DG .. g*DG+DG).
   float qf[DG];
@@ -369,7 +383,39 @@ __global__ void __launch_bounds__(256, (D == 64 && T > 0) ? 2 : 3) mhsea_fwd_ker
     float mut[TT];
 #pragma unroll
     for (int t = 0; t < T; ++t) mut[t] = group_sum(mu[t]) * inv;
-    if (qvalid) {
+    if (GATED && qvalid) {
+      const int64_t ybase = (static_cast<int64_t>(b) * N + qsite) * HG * D + static_cast<int64_t>(h0) * D;
+#pragma unroll
+      for (int dt = 0; dt < DT; ++dt) {
+        const int d0 = dt * 16 + 4 * g;
+        if (D % 16 != 0 && d0 >= D) continue;
+        float ov[4], tv[TT][4];
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          ov[r] = o[dt][r] * inv;
+#pragma unroll
+          for (int t = 0; t < T; ++t) tv[t][r] = (at[t][dt][r] + ct[t][dt][r]) * inv - mut[t] * ov[r];
+        }
+        if (pass == 0) {
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            const float sg = __builtin_amdgcn_rcpf(1.f + fast_exp2(-kLog2e * ov[r]));
+            gs[dt][r] = sg;
+#pragma unroll
+            for (int t = 0; t < T; ++t) gd[t][dt][r] = sg * (1.f - sg) * tv[t][r];
+          }
+        } else {
+          store4<F32>(p.out, ybase + d0, gs[dt][0] * ov[0], gs[dt][1] * ov[1], gs[dt][2] * ov[2], gs[dt][3] * ov[3]);
+#pragma unroll
+          for (int t = 0; t < T; ++t) {
+            float yd[4];
+#pragma unroll
+            for (int r = 0; r < 4; ++r) yd[r] = gd[t][dt][r] * ov[r] + gs[dt][r] * tv[t][r];
+            store4<F32>(p.tout, t * p.y_tstride + ybase + d0, yd[0], yd[1], yd[2], yd[3]);
+          }
+        }
+      }
+    } else if (qvalid) {
       const int64_t obase = bnhd(b, qsite, h, N, H, D);
 #pragma unroll
       for (int dt = 0; dt < DT; ++dt) {
@@ -401,11 +447,25 @@ __global__ void __launch_bounds__(256, (D == 64 && T > 0) ? 2 : 3) mhsea_fwd_ker
       }
     }
   }
+  }  // pass
 
   // Rows of masked queries (square mask only) are exact zeros; lse takes the value the
   // reference's all -1e4 row produces, -1e4 + log(N). Decided from the LDS copy of the
   // mask, after the compute so these stores never delay a load.
-  if (!p.key_mask) {
+  if (GATED && !p.key_mask) {
+    const int r0 = blk * 64;
+    for (int it = tid; it < 64 * C4; it += 256) {
+      const int r = r0 + it / C4;
+      const int c4 = it % C4;
+      if (r < N && mask_s[r] == 0) {
+        const int64_t off = (static_cast<int64_t>(b) * N + r) * HG * D + static_cast<int64_t>(h0) * D + c4 * 4;
+        store4<F32>(p.out, off, 0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+        for (int t = 0; t < T; ++t) store4<F32>(p.tout, t * p.y_tstride + off, 0.f, 0.f, 0.f, 0.f);
+      }
+    }
+  } else if (!p.key_mask) {
+    const int h = h0;
     const int r0 = blk * 64;
     for (int it = tid; it < 64 * C4; it += 256) {
       const int r = r0 + it / C4;
@@ -422,13 +482,13 @@ __global__ void __launch_bounds__(256, (D == 64 && T > 0) ? 2 : 3) mhsea_fwd_ker
   }
 }
 
-template <int D, int T, bool GIVEN_LSE, bool HAS_E, class S>
+template <int D, int T, bool GIVEN_LSE, bool HAS_E, class S, bool GATED = false>
 hipError_t launch_fwd_t(const FwdParams& p, hipStream_t stream) {
   const int nblk = (p.N + 63) / 64;
-  const int64_t nwg = static_cast<int64_t>(p.B) * p.H * nblk;
+  const int64_t nwg = static_cast<int64_t>(p.B) * (GATED ? p.H / 2 : p.H) * nblk;
   const size_t lds = FwdShape<D, T>::lds_bytes(p.N);
-  auto kern = p.N > FwdShape<D, T>::KC ? mhsea_fwd_kernel<D, T, GIVEN_LSE, HAS_E, S, true>
-                                       : mhsea_fwd_kernel<D, T, GIVEN_LSE, HAS_E, S, false>;
+  auto kern = p.N > FwdShape<D, T>::KC ? mhsea_fwd_kernel<D, T, GIVEN_LSE, HAS_E, S, true, GATED>
+                                       : mhsea_fwd_kernel<D, T, GIVEN_LSE, HAS_E, S, false, GATED>;
   if (lds > 64 * 1024) {
     hipError_t err = hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
                                          hipFuncAttributeMaxDynamicSharedMemorySize,
@@ -455,6 +515,17 @@ hipError_t dispatch_t(const FwdParams& p, int T, bool given_lse, hipStream_t str
   if (T == 0) return dispatch_e<D, 0, false, S>(p, stream);
   if (T == 1) return dispatch_e<D, 1, false, S>(p, stream);
   if (T == 2) return dispatch_e<D, 2, false, S>(p, stream);
+  return hipErrorInvalidValue;
+}
+
+template <int D>
+hipError_t dispatch_gated(const FwdParams& p, int T, hipStream_t stream) {
+  const bool e = p.e != nullptr;
+  if (T == 0) return e ? launch_fwd_t<D, 0, false, true, F32, true>(p, stream) : launch_fwd_t<D, 0, false, false, F32, true>(p, stream);
+  if (T == 1) return e ? launch_fwd_t<D, 1, false, true, F32, true>(p, stream) : launch_fwd_t<D, 1, false, false, F32, true>(p, stream);
+  if constexpr (D < 32) {  // two directions per launch only where their gate terms fit the registers
+    if (T == 2) return e ? launch_fwd_t<D, 2, false, true, F32, true>(p, stream) : launch_fwd_t<D, 2, false, false, F32, true>(p, stream);
+  }
   return hipErrorInvalidValue;
 }
 
@@ -492,6 +563,16 @@ hipError_t device_cu_count(int* cus) {
   if (dev >= 0 && dev < kMaxDevices) cached[dev].store(n, std::memory_order_relaxed);
   *cus = n;
   return hipSuccess;
+}
+
+hipError_t launch_fwd_gated_generic(const FwdParams& p, int D, int T, hipStream_t stream) {
+  switch (D) {
+    case 8: return dispatch_gated<8>(p, T, stream);
+    case 16: return dispatch_gated<16>(p, T, stream);
+    case 32: return dispatch_gated<32>(p, T, stream);
+    case 64: return dispatch_gated<64>(p, T, stream);
+    default: return hipErrorInvalidValue;
+  }
 }
 
 hipError_t launch_fwd(const FwdParams& p, int D, int T, bool given_lse, int dtype,

@@ -30,7 +30,7 @@ struct FwdParams {
   int key_mask;  // 1: reference_edge_attention masking (keys only)
   float masked_lse;
   int force_generic;  // 1: always use the LDS-streaming kernel
-  // 1: gated head collapse (producer/consumer kernel only): out is y [B, N, H/2, D] =
+  // 1: gated head collapse (producer/consumer and LDS-streaming fp32 kernels): out is y [B, N, H/2, D] =
   // sigmoid(O[:, :, h]) * O[:, :, h + H/2], tout its tangents [T, B, N, H/2, D] with
   // y_tstride elements between directions; lse is not written
   int gated;
@@ -92,6 +92,9 @@ hipError_t launch_fwd_bf16(const FwdParams& p, int D, int T, bool given_lse, hip
 // Producer/consumer kernel (float32, N <= 64): key tiles gathered into LDS.
 bool pc_fwd_supported(int N, int H, int D, int T, int dtype);
 hipError_t launch_fwd_pc(const FwdParams& p, int D, int T, bool given_lse, hipStream_t stream);
+// The gated collapse on the LDS-streaming fp32 kernel (any N, D): p.gated layout as above,
+// T <= 2 in one launch.
+hipError_t launch_fwd_gated_generic(const FwdParams& p, int D, int T, hipStream_t stream);
 // Compute units of the current device (cached per device).
 hipError_t device_cu_count(int* cus);
 hipError_t launch_fwd_small(const FwdParams& p, int D, int T, bool given_lse, int dtype,

@@ -245,13 +245,14 @@ def mhsea_fwd_jvp_gated(
     scale: float = 1.0,
     key_mask: bool = False,
     e_layout: str = "qhk",
+    generic: bool = False,
 ) -> Tuple[Tensor, Optional[Tensor]]:
     """Fused forward (+ tangents) with the trunk's sigmoid-gate head collapse in the epilogue
     (``trunk.py:134-137``): head h < H/2 gates head h + H/2. Returns ``(y, ty)`` with
     ``y = sigmoid(out[:, :, :H/2]) * out[:, :, H/2:]`` of shape ``[B, N, H/2, D]`` and its
     forward-mode tangents (``[T, B, N, H/2, D]`` for batched tangents, ``[B, N, H/2, D]``
-    for one, None when no tangent is given). Serves fp32, N <= 64, D in {8, 16, 32}, even H,
-    at most two tangent directions."""
+    for one, None when no tangent is given). Serves fp32, any N and head dimension, even H,
+    at most two tangent directions (``generic`` forces the LDS-streaming kernel)."""
     B, N, H, D = _check_primals(q, k, v, mask, e, e_layout)
     if q.dtype != torch.float32:
         raise TypeError(f"the gated collapse computes in float32, got {q.dtype}")
@@ -271,7 +272,7 @@ def mhsea_fwd_jvp_gated(
         _native.lib().hz_mhsea_fwd_jvp_gated(
             _stream(q.device), _ptr(q), _ptr(k), _ptr(e), _ptr(v), _ptr(m),
             _ptr(qt), _ptr(kt), _ptr(et), _ptr(vt), T, _ptr(y), _ptr(ty),
-            B, N, H, D, float(scale), _flags(key_mask, e_layout, False),
+            B, N, H, D, float(scale), _flags(key_mask, e_layout, generic),
         )
     )
     return y, (None if ty is None else (ty if batched else ty[0]))

@@ -174,7 +174,7 @@ class _GatedAD(torch.autograd.Function):
 def gated_edge_attention(q, k, e, v, mask, *, scale: float = 1.0, key_mask: bool = False, e_layout: str = "qhk"):
     """Differentiable head-collapsed attention ``sigmoid(gate) * value`` (trunk.py:130-137 for
     the tuned path): ``[B, N, H, D]`` operands with H = 2 * n_heads, result ``[B, N, H/2, D]``.
-    Serves what ``hz_mhsea_fwd_jvp_gated`` serves (fp32, N <= 64, D in {8, 16, 32})."""
+    Serves what ``hz_mhsea_fwd_jvp_gated`` serves (fp32, any N and head dimension, even H)."""
     return _GatedAD.apply(q, k, e, v, mask, (float(scale), bool(key_mask), e_layout))
 
 

@@ -148,8 +148,10 @@ int hz_mhsea_fwd_jvp(hipStream_t stream,
  * where out and tout[t] are what hz_mhsea_fwd_jvp computes. Head h < H/2 is the gate of
  * head h + H/2. Writes y [B, N, H/2, D] and ty [T, B, N, H/2, D] (masked query rows 0);
  * out, lse and the per-head tangents never reach memory.
- * Served shapes (the producer/consumer kernel): fp32, N <= 64, D in {8, 16, 32}, H even,
- * 0 <= T <= 2 (at D = 32 two directions run as two passes); others return HZ_EINVAL. Required: q, k, v, mask, y, and ty when T >= 1.
+ * Served shapes: fp32, any N <= HZ_MAX_N and D, H even, 0 <= T <= 2 (N <= 64 and D <= 32 on
+ * the producer/consumer kernel, at D = 32 two directions as two passes; otherwise, and with
+ * HZ_FLAG_GENERIC, on the LDS-streaming kernel, which computes the gate head and then the
+ * value head of each query block in one workgroup). Required: q, k, v, mask, y, and ty when T >= 1.
  * Optional: e, qt, kt, et, vt (tangent strides B*N*H*D; ty's stride is B*N*(H/2)*D).
  */
 int hz_mhsea_fwd_jvp_gated(hipStream_t stream,

@@ -60,6 +60,13 @@ CASES = [
     (11, 25, 64, 8, 8, 1, "prefix", True, True, "qhk"),
     # the trunk's own call: n_heads 16 doubled for the gate, d_head 256 / 16 (config.py:20,26)
     (12, 48, 64, 32, 16, 2, "prefix", False, True, "qkh"),
+    # N > 64 and D = 64: the LDS-streaming kernel (gate head, then value head, per block)
+    (13, 6, 100, 4, 32, 2, "scattered", False, True, "qhk"),
+    (14, 3, 256, 2, 64, 1, "counts", False, True, "qkh"),
+    (15, 4, 130, 8, 16, 2, "prefix", True, True, "qhk"),
+    (16, 5, 96, 6, 8, 0, "scattered", False, False, "qhk"),
+    (17, 2, 300, 4, 64, 2, "scattered", False, False, "qhk"),
+    (18, 7, 64, 4, 64, 1, "prefix", False, True, "qhk"),
 ]
 
 
@@ -193,3 +200,30 @@ def test_gated_then_out_proj_at_the_trunk_shape():
     wy, wty = O.gated_fwd_jvp(q, k, e, v, mask, tq[0], tk[0], te[0], tv[0], scale=0.25)
     assert rel(delta.cpu().numpy(), O.out_proj(wy, w)) <= TOL
     assert rel(dt[0].cpu().numpy(), O.out_proj(wty, w)) <= TOL
+
+
+
+@pytest.mark.parametrize("case", [(21, 9, 64, 8, 32, 2, "scattered", False, True, "qhk"),
+                                  (22, 20, 40, 4, 16, 2, "counts", True, True, "qkh"),
+                                  (23, 300, 64, 4, 8, 1, "prefix", False, False, "qhk")])
+def test_gated_forced_generic_matches_oracle(case):
+    """HZ_FLAG_GENERIC routes shapes the producer/consumer kernel serves to the LDS-streaming
+    gated kernel; same oracle, same tolerance."""
+    from hamiltonzero_amd import kernels
+
+    seed, B, N, H, D, T, mask_kind, key_mask, with_e, e_layout = case
+    _say(f"gated generic {case}")
+    q, k, v, e, mask, tq, tk, tv, te = make(seed, B, N, H, D, T, mask_kind, with_e, e_layout)
+    dev = lambda x: None if x is None else torch.from_numpy(x).cuda()  # noqa: E731
+    kw = dict(scale=D ** -0.5, key_mask=key_mask, e_layout=e_layout, generic=True)
+    y, ty = kernels.mhsea_fwd_jvp_gated(dev(q), dev(k), dev(v), dev(mask), dev(tq[:T]), dev(tk[:T]), dev(tv[:T]),
+                                        e=dev(e), et=None if te is None else dev(te[:T]), **kw)
+    torch.cuda.synchronize()
+    kw.pop("generic")
+    for t in range(T):
+        ey, eyd = O.gated_fwd_jvp(q, k, e, v, mask, tq[t], tk[t], None if te is None else te[t], tv[t], **kw)
+        if t == 0:
+            assert rel(y.cpu().numpy(), ey) <= TOL
+            if not key_mask:
+                assert np.all(y.cpu().numpy()[~mask] == 0.0)
+        assert rel(ty[t].cpu().numpy(), eyd) <= TOL
