@@ -36,6 +36,7 @@ EXPORTED_SYMBOLS = (
     "hz_mhsea_fwd_jvp_gated",
     "hz_mhsea_bwd",
     "hz_gated_out_proj",
+    "hz_mhsea_bwd_gated",
     "hz_rect_attention_fwd",
     "hz_quadrilinear_merge",
     "hz_factorized_apply",
@@ -100,6 +101,8 @@ _SIGNATURES = {
     "hz_factorized_apply_noalloc": ([_P, _P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64], _INT),
     # stream, y, ty, w_o, mask, delta, delta_t, B, N, d_attn, d_e, T
     "hz_gated_out_proj": ([_P] * 7 + [_I64] * 5, _INT),
+    # stream, q, k, e, v, mask, lse, out, dy, dq, dk, de, dv, dout_work, B, N, H, D, scale, flags
+    "hz_mhsea_bwd_gated": ([_P] * 14 + [_I64] * 4 + [_F, _INT], _INT),
     # B, n_sites, d_z, R_leaf, d_m, R_merge, R_out
     "hz_compiled_wavefunction_workspace": ([_I64] * 7, _I64),
     # stream, q, q_weight, leaf_V, leaf_U, leaf_h, merge_T, merge_V, merge_U, merge_h, opcodes,

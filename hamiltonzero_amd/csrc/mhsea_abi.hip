@@ -591,4 +591,20 @@ int hz_gated_out_proj(hipStream_t stream, const float* y, const float* ty, const
   return 0;
 }
 
+int hz_mhsea_bwd_gated(hipStream_t stream, const void* q, const void* k, const void* e, const void* v,
+                       const uint8_t* mask, const float* lse, const void* out, const float* dy, void* dq, void* dk,
+                       void* de, void* dv, float* dout_work, int64_t B, int64_t N, int64_t H, int64_t D, float scale,
+                       int flags) {
+  if (int rc = check_dims(B, N, H, D, HZ_DTYPE_F32, flags)) return rc;
+  if (H % 2 != 0) return fail(HZ_EINVAL, "the gated collapse pairs head h with h + H/2: H must be even, got %lld", (long long)H);
+  HZ_REQUIRE(out);
+  HZ_REQUIRE(dy);
+  HZ_REQUIRE(dout_work);
+  if (int rc = launched(hz::launch_gate_collapse_bwd(static_cast<const float*>(out), dy, dout_work, B * N,
+                                                     static_cast<int>(H), static_cast<int>(D), stream)))
+    return rc;
+  return hz_mhsea_bwd(stream, q, k, e, v, mask, lse, out, dout_work, dq, dk, de, dv, B, N, H, D, HZ_DTYPE_F32, scale,
+                      flags);
+}
+
 }  // extern "C"

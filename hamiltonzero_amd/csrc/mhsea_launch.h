@@ -95,6 +95,10 @@ hipError_t launch_fwd_pc(const FwdParams& p, int D, int T, bool given_lse, hipSt
 // The gated collapse on the LDS-streaming fp32 kernel (any N, D): p.gated layout as above,
 // T <= 2 in one launch.
 hipError_t launch_fwd_gated_generic(const FwdParams& p, int D, int T, hipStream_t stream);
+// dout [B, N, H, D] of the attention from the collapse's cotangent dy [B, N, H/2, D] and the
+// attention output out [B, N, H, D] (gate_bwd.hip), fp32, D a multiple of 4.
+hipError_t launch_gate_collapse_bwd(const float* out, const float* dy, float* dout, int64_t sites, int H, int D,
+                                    hipStream_t stream);
 // Compute units of the current device (cached per device).
 hipError_t device_cu_count(int* cus);
 hipError_t launch_fwd_small(const FwdParams& p, int D, int T, bool given_lse, int dtype,

@@ -317,6 +317,48 @@ def gated_out_proj(y: Tensor, w_o: Tensor, ty: Optional[Tensor] = None,
     return delta, (None if delta_t is None else (delta_t if batched else delta_t[0]))
 
 
+def mhsea_bwd_gated(
+    q: Tensor,
+    k: Tensor,
+    v: Tensor,
+    mask: Tensor,
+    lse: Tensor,
+    out: Tensor,
+    dy: Tensor,
+    e: Optional[Tensor] = None,
+    *,
+    want_de: bool = True,
+    scale: float = 1.0,
+    key_mask: bool = False,
+    e_layout: str = "qhk",
+) -> Tuple[Tensor, Tensor, Optional[Tensor], Tensor]:
+    """Reverse mode of the gated head collapse: ``(dq, dk, de, dv)`` for the cotangent
+    ``dy [B, N, H/2, D]`` of ``y = sigmoid(out[:, :, :H/2]) * out[:, :, H/2:]``, given the
+    attention's ``(out, lse)`` (``hz_mhsea_bwd_gated``: the collapse's cotangent formed on
+    the GPU, then the attention backward). float32."""
+    B, N, H, D = _check_primals(q, k, v, mask, e, e_layout)
+    if q.dtype != torch.float32:
+        raise TypeError(f"the gated collapse computes in float32, got {q.dtype}")
+    if H % 2:
+        raise ValueError(f"the gated collapse pairs head h with h + H/2: H must be even, got {H}")
+    if tuple(out.shape) != (B, N, H, D) or tuple(dy.shape) != (B, N, H // 2, D) or tuple(lse.shape) != (B, N, H):
+        raise ValueError("out must be [B, N, H, D], dy [B, N, H/2, D] and lse [B, N, H]")
+    _on_device(q.device, lse=lse, out=out, dy=dy)
+    q, k, v, e, lse, out, dy = _c(q), _c(k), _c(v), _c(e), _c(lse), _c(out), _c(dy)
+    m = _mask_u8(mask, q.device)
+    dq, dk, dv = torch.empty_like(q), torch.empty_like(k), torch.empty_like(v)
+    de = torch.empty_like(e) if (want_de and e is not None) else None
+    work = torch.empty_like(out)
+    _native.check(
+        _native.lib().hz_mhsea_bwd_gated(
+            _stream(q.device), _ptr(q), _ptr(k), _ptr(e), _ptr(v), _ptr(m), _ptr(lse), _ptr(out), _ptr(dy),
+            _ptr(dq), _ptr(dk), _ptr(de), _ptr(dv), _ptr(work), B, N, H, D, float(scale),
+            _flags(key_mask, e_layout, False),
+        )
+    )
+    return dq, dk, de, dv
+
+
 def mhsea_bwd(
     q: Tensor,
     k: Tensor,

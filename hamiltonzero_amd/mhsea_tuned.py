@@ -132,8 +132,9 @@ class _MhseaAD(torch.autograd.Function):
 class _GatedAD(torch.autograd.Function):
     """y = sigmoid(out[:, :, :H/2]) * out[:, :, H/2:] of MHSEA(q, k, e, v, mask), the trunk's
     head collapse (trunk.py:134-137). The forward and forward mode run the fused kernel
-    (``hz_mhsea_fwd_jvp_gated``); reverse mode recomputes (out, lse), forms the collapse's
-    cotangent per head and runs the attention backward on it."""
+    (``hz_mhsea_fwd_jvp_gated``); reverse mode recomputes (out, lse) and runs
+    ``hz_mhsea_bwd_gated`` (the collapse's cotangent formed on the GPU, then the attention
+    backward)."""
 
     @staticmethod
     def forward(q, k, e, v, mask, opts):
@@ -153,11 +154,8 @@ class _GatedAD(torch.autograd.Function):
         q, k, e, v, mask = ctx.saved_tensors
         scale, key_mask, e_layout = ctx.opts
         out, lse = kernels.mhsea_fwd(q, k, v, mask, e, scale=scale, key_mask=key_mask, e_layout=e_layout)
-        hh = out.shape[2] // 2
-        s = torch.sigmoid(out[:, :, :hh])
-        dout = torch.cat([dy * out[:, :, hh:] * s * (1 - s), dy * s], dim=2)
-        dq, dk, de, dv = kernels.mhsea_bwd(
-            q, k, v, mask, lse, out, dout, e,
+        dq, dk, de, dv = kernels.mhsea_bwd_gated(
+            q, k, v, mask, lse, out, dy.contiguous(), e,
             want_de=bool(ctx.needs_input_grad[2]), scale=scale, key_mask=key_mask, e_layout=e_layout,
         )
         return dq, dk, de, dv, None, None

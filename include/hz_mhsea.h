@@ -193,6 +193,23 @@ int hz_mhsea_bwd(hipStream_t stream,
                  int dtype, float scale, int flags);
 
 /*
+ * Reverse mode of the gated head collapse (hz_mhsea_fwd_jvp_gated's y = sigmoid(g) v):
+ * cotangents of (q, k, e, v) for the cotangent dy [B, N, H/2, D] of y. Replaces the reverse
+ * pass JAX derives for the trunk's attention call followed by trunk.py:134-137 (the
+ * collapse's VJP, then _inner_transpose, mhsea_tuned.py:206-221):
+ *     dout[:, :, h]       = dy[:, :, h] v sigmoid(g) (1 - sigmoid(g)),   g = out[:, :, h]
+ *     dout[:, :, h + H/2] = dy[:, :, h] sigmoid(g),                      v = out[:, :, h + H/2]
+ * then exactly hz_mhsea_bwd on dout. out [B, N, H, D] and lse are the attention's primal
+ * outputs (hz_mhsea_fwd); dout_work [B, N, H, D] is caller-owned scratch that receives dout.
+ * float32 only; H even; other operands and semantics as hz_mhsea_bwd.
+ */
+int hz_mhsea_bwd_gated(hipStream_t stream,
+                       const void* q, const void* k, const void* e, const void* v,
+                       const uint8_t* mask, const float* lse, const void* out, const float* dy,
+                       void* dq, void* dk, void* de, void* dv, float* dout_work,
+                       int64_t B, int64_t N, int64_t H, int64_t D, float scale, int flags);
+
+/*
  * Rectangular attention with a dense pair bias, forward only (the large-N evaluation
  * path). Replaces noncausal_bias_mha (src/hamiltonzero/evaluation/pallas_mha.py:92-161,
  * kernel :43-89) and its wrapper pallas_rectangular_edge_attention

@@ -224,6 +224,18 @@ def gated_fwd_jvp(q, k, e, v, mask, qt, kt, et, vt, *, scale=1.0, key_mask=False
     return y, ydot
 
 
+def gated_vjp(q, k, e, v, mask, dy, *, scale=1.0, key_mask=False, e_layout="qhk"):
+    """(dq, dk, de, dv): reverse mode of ``gate_collapse`` after ``fwd``, for the cotangent
+    ``dy [B, N, H/2, D]`` of y: the collapse's cotangent per head (gate: dy v s (1 - s), value:
+    dy s, s = sigmoid(gate), trunk.py:136) fed to ``vjp``."""
+    out, _ = fwd(q, k, e, v, mask, scale=scale, key_mask=key_mask, e_layout=e_layout)
+    hh = out.shape[2] // 2
+    s = 1.0 / (1.0 + np.exp(-out[:, :, :hh]))
+    dy = _f64(dy)
+    dout = np.concatenate([dy * out[:, :, hh:] * s * (1.0 - s), dy * s], axis=2)
+    return vjp(q, k, e, v, mask, dout, scale=scale, key_mask=key_mask, e_layout=e_layout)
+
+
 def out_proj(y, w_o, mask=None):
     """The attention block's output projection after the collapse: ``y_flat @ w_o``
     (trunk.py:138-144), times ``mask_q`` when a site mask is given (tree.py:1479-1488).

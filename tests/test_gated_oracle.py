@@ -99,3 +99,20 @@ def test_out_proj_matches_loops_and_masks_rows():
             assert np.allclose(got[b, i], want, rtol=1e-13, atol=1e-13)
     assert np.all(got[~mask] == 0.0)
     assert np.allclose(O.out_proj(y, w), np.einsum("bihd,hdj->bij", y, w.reshape(2, 4, 5)), rtol=1e-13)
+
+
+def test_gated_vjp_is_the_transpose_of_the_pinned_jvp():
+    """<ydot(t), dy> = <t, gated_vjp(dy)> for random tangents t of (q, k, e, v): the reverse
+    mode is the adjoint of the forward mode pinned above by central differences."""
+    rng = np.random.default_rng(43)
+    B, N, H, D = 2, 7, 4, 8
+    q, k, v, qt, kt, vt = (rng.standard_normal((B, N, H, D)) * 0.5 for _ in range(6))
+    e, et = (rng.standard_normal((B, N, H, N)) * 0.5 for _ in range(2))
+    mask = rng.random((B, N)) < 0.7
+    mask[:, 0] = True
+    dy = rng.standard_normal((B, N, H // 2, D))
+    _, ydot = O.gated_fwd_jvp(q, k, e, v, mask, qt, kt, et, vt, scale=0.3)
+    dq, dk, de, dv = O.gated_vjp(q, k, e, v, mask, dy, scale=0.3)
+    lhs = np.sum(ydot * dy)
+    rhs = np.sum(dq * qt) + np.sum(dk * kt) + np.sum(de * et) + np.sum(dv * vt)
+    assert abs(lhs - rhs) <= 1e-10 * max(1.0, abs(lhs))

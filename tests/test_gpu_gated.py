@@ -227,3 +227,28 @@ def test_gated_forced_generic_matches_oracle(case):
             if not key_mask:
                 assert np.all(y.cpu().numpy()[~mask] == 0.0)
         assert rel(ty[t].cpu().numpy(), eyd) <= TOL
+
+
+@pytest.mark.parametrize("case", [(31, 16, 64, 8, 32, "scattered", False, True, "qhk"),
+                                  (32, 6, 100, 4, 16, "counts", True, True, "qkh"),
+                                  (33, 48, 64, 32, 16, "prefix", False, False, "qhk")])
+def test_gated_bwd_matches_oracle(case):
+    """hz_mhsea_bwd_gated (the collapse's cotangent on the GPU, then the attention backward)
+    against the oracle's gated_vjp, pinned as the adjoint of the pinned forward mode."""
+    from hamiltonzero_amd import kernels
+
+    seed, B, N, H, D, mask_kind, key_mask, with_e, e_layout = case
+    _say(f"gated bwd {case}")
+    q, k, v, e, mask, *_ = make(seed, B, N, H, D, 0, mask_kind, with_e, e_layout)
+    dy = np.random.default_rng(seed + 1).standard_normal((B, N, H // 2, D), dtype=np.float32)
+    dev = lambda x: None if x is None else torch.from_numpy(x).cuda()  # noqa: E731
+    kw = dict(scale=D ** -0.5, key_mask=key_mask, e_layout=e_layout)
+    out, lse = kernels.mhsea_fwd(dev(q), dev(k), dev(v), dev(mask), dev(e), **kw)
+    dq, dk, de, dv = kernels.mhsea_bwd_gated(dev(q), dev(k), dev(v), dev(mask), lse, out, dev(dy), dev(e),
+                                             want_de=with_e, **kw)
+    torch.cuda.synchronize()
+    want = O.gated_vjp(q, k, e, v, mask, dy, **kw)
+    for name, got, ref in zip(("dq", "dk", "de", "dv"), (dq, dk, de, dv), want):
+        if got is None:
+            continue
+        assert rel(got.cpu().numpy(), ref) <= TOL, name
