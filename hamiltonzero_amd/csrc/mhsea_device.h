@@ -287,4 +287,30 @@ __device__ __forceinline__ int64_t xcd_logical_block(int64_t hw, int64_t nblocks
   return (hw % kXcd) * per + hw / kXcd;
 }
 
+// Mask compaction for a workgroup of W waves (64 W threads): idx[0..count) = physical sites
+// (ascending), mask_s = the raw mask bytes. Returns count to every thread.
+template <int W>
+__device__ __forceinline__ int compact_mask_wg(const uint8_t* __restrict__ mask_row, int N, int16_t* __restrict__ idx,
+                                               uint8_t* __restrict__ mask_s, int* __restrict__ scratch) {
+  const int tid = threadIdx.x;
+  const int wave = tid >> 6;
+  const int lane = tid & 63;
+  int total = 0;
+  for (int base = 0; base < N; base += (64 * W)) {
+    const int pos = base + tid;
+    const uint8_t m = pos < N ? mask_row[pos] : 0;
+    if (pos < N) mask_s[pos] = m;
+    const bool on = m != 0;
+    const uint64_t bal = __ballot(on);
+    if (lane == 0) scratch[wave] = __popcll(bal);
+    __syncthreads();
+    int before = total;
+    for (int w = 0; w < wave; ++w) before += scratch[w];
+    if (on) idx[before + __popcll(bal & ((uint64_t(1) << lane) - 1))] = static_cast<int16_t>(pos);
+    for (int w = 0; w < W; ++w) total += scratch[w];
+    __syncthreads();
+  }
+  return total;
+}
+
 }  // namespace hz

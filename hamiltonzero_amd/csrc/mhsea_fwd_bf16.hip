@@ -235,13 +235,15 @@ __global__ void __launch_bounds__(256, ((D == 64 && T > 0) ? 2 : 3)) mhsea_fwd_b
       qf[s] = as_bf16x8(*reinterpret_cast<const uint4*>(static_cast<const uint16_t*>(p.q) + qoff + 32 * s));
 #pragma unroll
       for (int t = 0; t < T; ++t)
-        qtf[t][s] = as_bf16x8(*reinterpret_cast<const uint4*>(static_cast<const uint16_t*>(qtp) + t * qts + qoff + 32 * s));
+        qtf[t][s] = has_qt ? as_bf16x8(*reinterpret_cast<const uint4*>(static_cast<const uint16_t*>(qtp) + t * qts + qoff + 32 * s))
+                           : bf16x8{};
     }
   }
   // Padding query lanes only produce values that are never stored; the scale is applied to
-  // the fp32 scores (exact in the product, no extra rounding of q).
+  // the fp32 scores (exact in the product, no extra rounding of q). A null qt contributes
+  // zero fragments, so dS = Kt Q^T alone keeps its scale.
   const float sscale = p.scale;
-  const float stscale = has_qt ? p.scale : 0.f;
+  const float stscale = p.scale;
   float lse2 = 0.f;
   if constexpr (GIVEN_LSE) lse2 = p.lse_in[(static_cast<int64_t>(b) * N + qload) * H + h] * kLog2e;
   const int64_t e_row = static_cast<int64_t>(b) * N * N * H + static_cast<int64_t>(qload) * p.e_sq +

@@ -104,31 +104,6 @@ struct LShape {
   }
 };
 
-// Mask compaction for a workgroup of kWaves waves: idx[0..count) = physical sites
-// (ascending), mask_s = the raw mask bytes. Returns count to every thread.
-__device__ __forceinline__ int compact_mask_wg(const uint8_t* __restrict__ mask_row, int N, int16_t* __restrict__ idx,
-                                               uint8_t* __restrict__ mask_s, int* __restrict__ scratch) {
-  const int tid = threadIdx.x;
-  const int wave = tid >> 6;
-  const int lane = tid & 63;
-  int total = 0;
-  for (int base = 0; base < N; base += kThreads) {
-    const int pos = base + tid;
-    const uint8_t m = pos < N ? mask_row[pos] : 0;
-    if (pos < N) mask_s[pos] = m;
-    const bool on = m != 0;
-    const uint64_t bal = __ballot(on);
-    if (lane == 0) scratch[wave] = __popcll(bal);
-    __syncthreads();
-    int before = total;
-    for (int w = 0; w < wave; ++w) before += scratch[w];
-    if (on) idx[before + __popcll(bal & ((uint64_t(1) << lane) - 1))] = static_cast<int16_t>(pos);
-    for (int w = 0; w < kWaves; ++w) total += scratch[w];
-    __syncthreads();
-  }
-  return total;
-}
-
 // HW_ID register (id 4, all 32 bits); the SIMD of the wave is bits 5:4.
 constexpr int kHwIdReg = 4 | (31 << 11);
 
@@ -164,7 +139,7 @@ __global__ void __launch_bounds__(kThreads, 1) mhsea_fwd_bf16_large_kernel(const
 
   // SIMD of each wave, published by the barriers of the mask compaction.
   if (lane == 0) scratch[8 + wave] = static_cast<int>((__builtin_amdgcn_s_getreg(kHwIdReg) >> 4) & 3);
-  const int n_phys = compact_mask_wg(p.mask + static_cast<int64_t>(b) * N, N, idx, mask_s, scratch);
+  const int n_phys = compact_mask_wg<kWaves>(p.mask + static_cast<int64_t>(b) * N, N, idx, mask_s, scratch);
   const bool key_all = p.key_mask && n_phys == 0;
   const int nk = key_all ? N : n_phys;
   const int nq = p.key_mask ? N : n_phys;
@@ -326,11 +301,11 @@ __global__ void __launch_bounds__(kThreads, 1) mhsea_fwd_bf16_large_kernel(const
       qf[s] = as_bf16x8(*reinterpret_cast<const uint4*>(static_cast<const uint16_t*>(p.q) + qoff + 32 * s));
 #pragma unroll
       for (int t = 0; t < T; ++t)
-        qtf[t][s] = as_bf16x8(*reinterpret_cast<const uint4*>(qt + t * qts + qoff + 32 * s));
+        qtf[t][s] = p.qt != nullptr ? as_bf16x8(*reinterpret_cast<const uint4*>(qt + t * qts + qoff + 32 * s)) : bf16x8{};
     }
   }
   const float sscale = p.scale;
-  const float stscale = p.qt != nullptr ? p.scale : 0.f;
+  const float stscale = p.scale;  // a null qt gives zero fragments: dS = Kt Q^T alone
   const float s2scale = sscale * kLog2e;
   float lse2 = 0.f;
   if constexpr (GIVEN_LSE) lse2 = p.lse_in[(static_cast<int64_t>(b) * N + qload) * H + h] * kLog2e;

@@ -115,6 +115,15 @@ CASES = [
     ("n200_bf16_d32_bias", 2, 200, 2, 32, 150, True, True, "qhk", False, 0.8, 1, True),
     ("n136_bf16_keymask_none", 2, 136, 1, 32, 0, False, False, "qhk", True, 1.0, 1, True),
     ("n256_bf16_mixed_t2", 6, 256, 2, 32, -1, True, True, "qhk", False, 1.0, 2, True),
+    # N > 128, bfloat16, D = 64, no bias: the 32-query-wave kernel (32-key chunks, the last
+    # one peeled off): one, two, an odd and an even number of chunks, a whole last chunk,
+    # a scale, the key mask with and without physical sites, walkers whose counts differ
+    ("n160_bf16_wide_one_chunk", 2, 160, 2, 64, 20, True, False, "qkh", True, 1.0, 1, True),
+    ("n256_bf16_wide_two_chunks", 2, 256, 2, 64, 50, True, False, "qhk", False, 1.0, 2, True),
+    ("n288_bf16_wide_scaled_t2", 4, 288, 3, 64, 260, True, False, "qhk", False, 0.125, 2, True),
+    ("n192_bf16_wide_whole_chunks", 3, 192, 2, 64, 160, True, False, "qhk", False, 1.0, 1, True),
+    ("n200_bf16_wide_keymask_none", 2, 200, 2, 64, 0, False, False, "qhk", True, 1.0, 2, True),
+    ("n320_bf16_wide_mixed", 8, 320, 2, 64, -1, True, False, "qhk", False, 1.0, 2, True),
 ]
 IDS = [c[0] for c in CASES]
 
@@ -299,3 +308,67 @@ def test_keymask_no_physical_key_gated():
                                         a["et"][t], a["vt"][t], key_mask=True)
         assert rel(host(y), ref_y) <= F32_TOL
         assert rel(host(ty)[t], ref_ty) <= F32_TOL
+
+
+# A null query tangent with a key tangent given: dS = Kt Q^T alone must keep its scale (the
+# bfloat16 kernels once zeroed the whole dS in this case). Every forward-kernel family:
+NULL_QT_CASES = [
+    # name, B, N, H, D, n_phys, with_e, scale, T, bf16
+    ("fp32_small_n16", 4, 16, 2, 16, 11, False, 0.5, 1, False),
+    ("fp32_pc_n64_d32", 8, 64, 4, 32, 36, False, 1.0, 2, False),
+    ("fp32_stream_n64_d64", 3, 64, 2, 64, 48, True, 0.7, 1, False),
+    ("fp32_lds_n256_d64", 2, 256, 2, 64, 200, False, 1.0, 1, False),
+    ("bf16_small_n64_d64", 4, 64, 2, 64, 48, False, 1.0, 2, True),
+    ("bf16_wide_n256_d64", 2, 256, 2, 64, 230, False, 1.0, 2, True),
+    ("bf16_wide_n256_d64_scaled", 2, 256, 2, 64, 230, False, 0.125, 1, True),
+    ("bf16_large_n200_d32_bias", 2, 200, 2, 32, 150, True, 0.8, 1, True),
+]
+
+
+@pytest.mark.parametrize("case", NULL_QT_CASES, ids=[c[0] for c in NULL_QT_CASES])
+def test_null_query_tangent(case):
+    from hamiltonzero_amd import kernels
+
+    name, B, N, H, D, n_phys, with_e, scale, T, bf16 = case
+    _say(f"null qt {name}")
+    a = make_inputs(zlib.crc32(name.encode()) % 1000, B, N, H, D, n_phys, scattered=True, with_e=with_e, T=T,
+                    bf16=bf16)
+    dt = torch.bfloat16 if bf16 else torch.float32
+    d = {n: to_dev(x, dt) for n, x in a.items()}
+    out, _, tout = kernels.mhsea_fwd_jvp(d["q"], d["k"], d["v"], d["mask"], None, d["kt"], d["vt"], d["e"], d["et"],
+                                         scale=scale)
+    torch.cuda.synchronize()
+    tol = BF16_TOL if bf16 else F32_TOL
+    zero = np.zeros_like(a["q"])
+    for t in range(T):
+        et = None if a["et"] is None else a["et"][t]
+        ref_t = O.jvp(a["q"], a["k"], a["e"], a["v"], a["mask"], zero, a["kt"][t], et, a["vt"][t], scale=scale)
+        assert rel(host(tout)[t], ref_t) <= tol, f"tangent {t}"
+
+
+def test_bf16_wide_matches_large_kernel_full_n():
+    """The 32-query-wave kernel (no bias) against the 16-query-wave kernel (reached with an
+    all-zero bias, the same mathematics) at c5's N and H, every walker's count different:
+    both are bf16 products with fp32 softmax, so they agree to bf16 rounding."""
+    from hamiltonzero_amd import kernels
+
+    _say("bf16 wide vs large N=1024 H=16")
+    B, N, H, D, T = 3, 1024, 16, 64, 2
+    g = torch.Generator(device="cuda").manual_seed(11)
+    r = lambda *s, sc=1.0: (torch.randn(*s, generator=g, device="cuda") * sc).to(torch.bfloat16)
+    q, k, v = r(B, N, H, D, sc=D ** -0.5), r(B, N, H, D, sc=D ** -0.5), r(B, N, H, D)
+    qt, kt, vt = r(T, B, N, H, D), r(T, B, N, H, D), r(T, B, N, H, D)
+    mask = torch.zeros(B, N, dtype=torch.bool, device="cuda")
+    for b, n in enumerate((1000, 777, 1024)):
+        mask[b, torch.randperm(N, generator=g, device="cuda")[:n]] = True
+    e0 = torch.zeros(B, N, H, N, dtype=torch.bfloat16, device="cuda")
+    o1, l1, t1 = kernels.mhsea_fwd_jvp(q, k, v, mask, qt, kt, vt)
+    o2, l2, t2 = kernels.mhsea_fwd_jvp(q, k, v, mask, qt, kt, vt, e0, torch.zeros(T, B, N, H, N, dtype=torch.bfloat16,
+                                                                                  device="cuda"))
+    torch.cuda.synchronize()
+    assert rel(host(o1), host(o2)) <= BF16_TOL
+    assert rel(host(l1), host(l2)) <= 1e-3  # the wide kernel normalises by its rounded weights
+    for t in range(T):
+        assert rel(host(t1)[t], host(t2)[t]) <= BF16_TOL, f"tangent {t}"
+    m = mask.cpu().numpy()
+    assert np.all(host(o1)[~m] == 0.0) and np.all(host(t1)[:, ~m] == 0.0)
