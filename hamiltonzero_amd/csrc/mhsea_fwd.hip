@@ -129,7 +129,7 @@ __device__ __forceinline__ void chunk_store(const float4 (&ck)[NPT], const float
 // sigma(g) and sigma'(g) gdot of its rows in registers between them, and writes only the
 // collapse y = sigma(g) v and ydot = sigma'(g) gdot v + sigma(g) vdot ([B, N, H/2, D]).
 template <int D, int T, bool GIVEN_LSE, bool HAS_E, class S, bool MULTI, bool GATED>
-__global__ void __launch_bounds__(256, ((D == 64 && T > 0) || (GATED && D >= 32)) ? 2 : 3)
+__global__ void __launch_bounds__(256, ((D == 64 && T > 0) || (D == 32 && T == 2) || (GATED && D >= 32)) ? 2 : 3)
     mhsea_fwd_kernel(const FwdParams p) {
   static_assert(!GATED || (!GIVEN_LSE && std::is_same<S, F32>::value), "the gated collapse is float32, no given lse");
   using Sh = FwdShape<D, T>;
