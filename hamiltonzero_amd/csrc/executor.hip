@@ -113,7 +113,10 @@ quadrilinear_merge_kernel(const float* __restrict__ T, const float* __restrict__
 // --------------------------------------------------------------------------------------
 constexpr int kBM = 128, kBN = 128, kBK = 16;
 // Row lengths of As[k][row] and Bs[k][col] (floats): 16 more than a tile, so the four k rows
-// of one operand read (lanes 16 g + c read row g, column c) fall on distinct banks.
+// of one operand read (lanes 16 g + c read row g, column c) fall on distinct banks. A's
+// transposed stores put column r of k rows 4q .. 4q + 3 at r ^ 16 q, so the four lanes that
+// share r (q = 0..3, rows 4 x 144 floats apart, one bank) write four banks; a read's four
+// rows share q, so it still covers one aligned 16-column block per row.
 constexpr int kAPad = kBM + 16;
 constexpr int kBPad = kBN + 16;
 
@@ -177,10 +180,13 @@ gemm_f32_kernel(const float* __restrict__ A, const float* __restrict__ Bm, float
     for (int u = 0; u < 2; ++u) {
       const int it = tid + 256 * u;
       const int r = it >> 2, k4 = 4 * (it & 3);
-      As[buf][k4 + 0][r] = ra[u].x;
-      As[buf][k4 + 1][r] = ra[u].y;
-      As[buf][k4 + 2][r] = ra[u].z;
-      As[buf][k4 + 3][r] = ra[u].w;
+      // column r of rows k4 .. k4 + 3 at r ^ 16 ((k4 / 4) mod 4): the four lanes sharing r
+      // (k4 = 0, 4, 8, 12) land in four banks instead of one
+      const int rs = r ^ (16 * ((k4 >> 2) & 3));
+      As[buf][k4 + 0][rs] = ra[u].x;
+      As[buf][k4 + 1][rs] = ra[u].y;
+      As[buf][k4 + 2][rs] = ra[u].z;
+      As[buf][k4 + 3][rs] = ra[u].w;
       *reinterpret_cast<float4*>(&Bs[buf][it >> 5][4 * (it & 31)]) = rb[u];
     }
   };
@@ -202,7 +208,7 @@ gemm_f32_kernel(const float* __restrict__ A, const float* __restrict__ Bm, float
     for (int ks = 0; ks < kBK; ks += 4) {
       float af[4], bf[4];
 #pragma unroll
-      for (int mt = 0; mt < 4; ++mt) af[mt] = As[buf][ks + g][wm + 16 * mt + c];
+      for (int mt = 0; mt < 4; ++mt) af[mt] = As[buf][ks + g][(wm + 16 * mt + c) ^ (16 * ((ks >> 2) & 3))];
 #pragma unroll
       for (int nt = 0; nt < 4; ++nt) bf[nt] = Bs[buf][ks + g][wn + 16 * nt + c];
 #pragma unroll
