@@ -90,6 +90,10 @@ hipError_t launch_fwd_bf16_large(const FwdParams& p, int D, int T, bool given_ls
 // 32x32x16 matrix instruction, one wave per SIMD; forward variants only, scale > 0.
 bool bf16_wide_fwd_supported(const FwdParams& p, int D, bool given_lse);
 hipError_t launch_fwd_bf16_wide(const FwdParams& p, int T, hipStream_t stream);
+// The same scope with each 32-query tile served by a score wave and a value wave (two waves
+// per SIMD, roles split).
+bool bf16_ws_fwd_supported(const FwdParams& p, int D, bool given_lse);
+hipError_t launch_fwd_bf16_ws(const FwdParams& p, int T, hipStream_t stream);
 bool bf16_bwd_supported(int N, int H, int D);
 hipError_t launch_bwd_bf16(const BwdParams& p, int D, hipStream_t stream);
 hipError_t launch_fwd_bf16(const FwdParams& p, int D, int T, bool given_lse, hipStream_t stream);
