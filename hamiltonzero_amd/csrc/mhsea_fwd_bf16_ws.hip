@@ -21,11 +21,11 @@
 // fragments and one chunk's scores (~190 registers), a value wave the accumulators and the
 // staging registers (~200), so two waves fit a SIMD. One workgroup barrier per chunk.
 //
-// Pipeline, iteration i: score waves compute S(i) from K(i) (K buffer i mod 3), the softmax,
-// and write W(i) (weights and rescale factors) into weight buffer i mod 2; value waves apply
-// W(i-1) to V(i-1) (weight and V buffers (i-1) mod 2), write K(i+2) into K buffer (i+2) mod 3
-// and V(i) into V buffer i mod 2 (both read from HBM in iteration i-1), and issue the reads of
-// K(i+3) and V(i+1). Every write goes to a buffer whose last reader finished before the
+// Pipeline, iteration i: score waves run the softmax of chunk i (scores computed in iteration
+// i-1) interleaved with the products of S(i+1) (K buffer (i+1) mod 3) and write W(i) (weights
+// and rescale factors) into weight buffer i mod 2; value waves apply W(i-1) to V(i-1) (weight
+// and V buffers (i-1) mod 2), write K(i+2) into K buffer (i+2) mod 3 and V(i) into V buffer
+// i mod 2 (both read from HBM in iteration i-1), and issue the reads of K(i+3) and V(i+1). Every write goes to a buffer whose last reader finished before the
 // previous barrier: K(i+2) replaces K(i-1) (read in iteration i-1), V(i) replaces V(i-2)
 // and W(i) replaces W(i-2) (both read in iteration i-1).
 //
@@ -276,11 +276,11 @@ __global__ void __launch_bounds__(kThreads, 1) mhsea_fwd_bf16_ws_kernel(const Fw
       float mu[TT];
 #pragma unroll
       for (int t = 0; t < T; ++t) mu[t] = 0.f;
-      __syncthreads();  // prologue: K(0), K(1) staged by the value waves
-      for (int i = 0; i < nc; ++i) {
-        // S(i) from K buffer i mod 3; order per k-step keeps products into one accumulator apart
-        const uint16_t* const kp = kbuf + (i % 3) * Sh::kKBuf + c * kKLD + 8 * hh;
-        v16f sc = zero16(), ds[TT];
+      // S(j) into (sc, ds) from K buffer j mod 3; the order per k-step keeps products into
+      // one accumulator apart
+      auto s_products = [&](int j, v16f& sc, v16f(&ds)[TT]) {
+        const uint16_t* const kp = kbuf + (j % 3) * Sh::kKBuf + c * kKLD + 8 * hh;
+        sc = zero16();
 #pragma unroll
         for (int t = 0; t < T; ++t) ds[t] = zero16();
 #pragma unroll
@@ -293,6 +293,10 @@ __global__ void __launch_bounds__(kThreads, 1) mhsea_fwd_bf16_ws_kernel(const Fw
 #pragma unroll
           for (int t = 0; t < T; ++t) ds[t] = mfma32(kf, qtf[t][s], ds[t]);
         }
+      };
+      // The softmax of chunk i (scores in sc, ds) with the products of S(i+1) (into scn, dsn,
+      // K(i+1) staged since the last barrier) interleaved between its vector instructions.
+      auto step = [&](int i, v16f& sc, v16f(&ds)[TT], v16f& scn, v16f(&dsn)[TT]) {
         // validity (only the last chunk holds padding keys), chunk maximum, base update
         if (i == nc - 1 && (nk & (kKC - 1)) != 0) {
 #pragma unroll
@@ -316,6 +320,8 @@ __global__ void __launch_bounds__(kThreads, 1) mhsea_fwd_bf16_ws_kernel(const Fw
           alpha = fast_exp2(m2 - mnew);  // 0 on the first chunk
           m2 = mnew;
         }
+        __builtin_amdgcn_sched_barrier(0);
+        s_products(i + 1, scn, dsn);
         // softmax weights, bf16, written where the partner lane reads them
         uint16_t* const wt = wtile0 + (i & 1) * Sh::kWBuf;
         float ls = 0.f, muc[TT];
@@ -342,11 +348,36 @@ __global__ void __launch_bounds__(kThreads, 1) mhsea_fwd_bf16_ws_kernel(const Fw
           }
         }
         if (hh == 0) atile0[(i & 1) * kPairs * kQW + c] = alpha;
+        // one product, then a run of vector instructions; the operand reads go out early
+        constexpr int kR = 4 * NX, kP = 4 * (1 + 2 * T);
+        __builtin_amdgcn_sched_group_barrier(0x100, 4, 0);
+#pragma unroll
+        for (int k = 0; k < kR - 4; ++k) {
+          __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+          __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+          __builtin_amdgcn_sched_group_barrier(0x002, 6, 0);
+        }
+#pragma unroll
+        for (int k = kR - 4; k < kP; ++k) {
+          __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+          __builtin_amdgcn_sched_group_barrier(0x002, 6, 0);
+        }
+        __builtin_amdgcn_sched_barrier(0);
         lsum = fmaf(lsum, alpha, ls);
 #pragma unroll
         for (int t = 0; t < T; ++t) mu[t] = fmaf(mu[t], alpha, muc[t]);
         __syncthreads();
+      };
+      v16f sA, sB, dA[TT], dB[TT];
+      __syncthreads();  // prologue: K(0), K(1) staged by the value waves
+      s_products(0, sA, dA);
+      int i = 0;
+#pragma clang loop unroll(disable)
+      for (; i + 1 < nc; i += 2) {
+        step(i, sA, dA, sB, dB);
+        step(i + 1, sB, dB, sA, dA);
       }
+      if (i < nc) step(i, sA, dA, sB, dB);
       // normaliser and tangent row sums for the value wave; lse
       // (the cross-half sums run with every lane active; only the writes are per half)
       const float ltot = xor32_pair_sum(lsum);
@@ -431,8 +462,8 @@ __global__ void __launch_bounds__(kThreads, 1) mhsea_fwd_bf16_ws_kernel(const Fw
       __syncthreads();
       for (int i = 0; i < nc; ++i) {
         if (i > 0) pv_step(i - 1);
-        // K(i+2) into K buffer (i+2) mod 3 (last read: K(i-1) in iteration i-1), V(i) into
-        // V buffer i mod 2 (last read: V(i-2) in iteration i-1), then the next reads
+        // K(i+2) into K buffer (i+2) mod 3 (last read: K(i-1), in iteration i-1), V(i) into
+        // V buffer i mod 2 (last read: V(i-2), in iteration i-1), then the next reads
         kstore((i + 2) % 3, rk);
         vstore(i & 1, rv);
         stage_loads((i + 3) * kKC, (i + 1) * kKC, rk, rv);
