@@ -579,7 +579,6 @@ hipError_t launch_fwd(const FwdParams& p, int D, int T, bool given_lse, int dtyp
                       hipStream_t stream) {
   if (!p.force_generic) {
     if (dtype == 1 && bf16_ws_fwd_supported(p, D, given_lse)) return launch_fwd_bf16_ws(p, T, stream);
-    if (dtype == 1 && bf16_wide_fwd_supported(p, D, given_lse)) return launch_fwd_bf16_wide(p, T, stream);
     if (dtype == 1 && bf16_large_fwd_supported(p.N, D)) return launch_fwd_bf16_large(p, D, T, given_lse, stream);
     if (dtype == 1 && bf16_fwd_supported(D)) return launch_fwd_bf16(p, D, T, given_lse, stream);
     if (small_fwd_supported(p.N, D, T)) return launch_fwd_small(p, D, T, given_lse, dtype, stream);

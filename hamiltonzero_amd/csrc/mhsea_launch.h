@@ -86,12 +86,9 @@ bool bf16_fwd_supported(int D);
 // Large-N bfloat16 kernel (N > 128): 128-query workgroups, double-buffered LDS key chunks.
 bool bf16_large_fwd_supported(int N, int D);
 hipError_t launch_fwd_bf16_large(const FwdParams& p, int D, int T, bool given_lse, hipStream_t stream);
-// Large-N bfloat16 kernel at D = 64 without a bias (N > 128): 32-query waves on the
-// 32x32x16 matrix instruction, one wave per SIMD; forward variants only, scale > 0.
-bool bf16_wide_fwd_supported(const FwdParams& p, int D, bool given_lse);
-hipError_t launch_fwd_bf16_wide(const FwdParams& p, int T, hipStream_t stream);
-// The same scope with each 32-query tile served by a score wave and a value wave (two waves
-// per SIMD, roles split).
+// Large-N bfloat16 kernel at D = 64 without a bias (N > 128): 32-query tiles on the 32x32x16
+// matrix instruction, each served by a score wave and a value wave (two waves per SIMD);
+// forward variants only, scale > 0.
 bool bf16_ws_fwd_supported(const FwdParams& p, int D, bool given_lse);
 hipError_t launch_fwd_bf16_ws(const FwdParams& p, int T, hipStream_t stream);
 bool bf16_bwd_supported(int N, int H, int D);

@@ -115,15 +115,15 @@ CASES = [
     ("n200_bf16_d32_bias", 2, 200, 2, 32, 150, True, True, "qhk", False, 0.8, 1, True),
     ("n136_bf16_keymask_none", 2, 136, 1, 32, 0, False, False, "qhk", True, 1.0, 1, True),
     ("n256_bf16_mixed_t2", 6, 256, 2, 32, -1, True, True, "qhk", False, 1.0, 2, True),
-    # N > 128, bfloat16, D = 64, no bias: the 32-query-wave kernel (32-key chunks, the last
-    # one peeled off): one, two, an odd and an even number of chunks, a whole last chunk,
+    # N > 128, bfloat16, D = 64, no bias: the 32-query-tile kernel (32-key chunks, the last
+    # one partial or whole): one, two, an odd and an even number of chunks, a whole last chunk,
     # a scale, the key mask with and without physical sites, walkers whose counts differ
-    ("n160_bf16_wide_one_chunk", 2, 160, 2, 64, 20, True, False, "qkh", True, 1.0, 1, True),
-    ("n256_bf16_wide_two_chunks", 2, 256, 2, 64, 50, True, False, "qhk", False, 1.0, 2, True),
-    ("n288_bf16_wide_scaled_t2", 4, 288, 3, 64, 260, True, False, "qhk", False, 0.125, 2, True),
-    ("n192_bf16_wide_whole_chunks", 3, 192, 2, 64, 160, True, False, "qhk", False, 1.0, 1, True),
-    ("n200_bf16_wide_keymask_none", 2, 200, 2, 64, 0, False, False, "qhk", True, 1.0, 2, True),
-    ("n320_bf16_wide_mixed", 8, 320, 2, 64, -1, True, False, "qhk", False, 1.0, 2, True),
+    ("n160_bf16_tile32_one_chunk", 2, 160, 2, 64, 20, True, False, "qkh", True, 1.0, 1, True),
+    ("n256_bf16_tile32_two_chunks", 2, 256, 2, 64, 50, True, False, "qhk", False, 1.0, 2, True),
+    ("n288_bf16_tile32_scaled_t2", 4, 288, 3, 64, 260, True, False, "qhk", False, 0.125, 2, True),
+    ("n192_bf16_tile32_whole_chunks", 3, 192, 2, 64, 160, True, False, "qhk", False, 1.0, 1, True),
+    ("n200_bf16_tile32_keymask_none", 2, 200, 2, 64, 0, False, False, "qhk", True, 1.0, 2, True),
+    ("n320_bf16_tile32_mixed", 8, 320, 2, 64, -1, True, False, "qhk", False, 1.0, 2, True),
 ]
 IDS = [c[0] for c in CASES]
 
@@ -319,8 +319,8 @@ NULL_QT_CASES = [
     ("fp32_stream_n64_d64", 3, 64, 2, 64, 48, True, 0.7, 1, False),
     ("fp32_lds_n256_d64", 2, 256, 2, 64, 200, False, 1.0, 1, False),
     ("bf16_small_n64_d64", 4, 64, 2, 64, 48, False, 1.0, 2, True),
-    ("bf16_wide_n256_d64", 2, 256, 2, 64, 230, False, 1.0, 2, True),
-    ("bf16_wide_n256_d64_scaled", 2, 256, 2, 64, 230, False, 0.125, 1, True),
+    ("bf16_tile32_n256_d64", 2, 256, 2, 64, 230, False, 1.0, 2, True),
+    ("bf16_tile32_n256_d64_scaled", 2, 256, 2, 64, 230, False, 0.125, 1, True),
     ("bf16_large_n200_d32_bias", 2, 200, 2, 32, 150, True, 0.8, 1, True),
 ]
 
@@ -346,13 +346,13 @@ def test_null_query_tangent(case):
         assert rel(host(tout)[t], ref_t) <= tol, f"tangent {t}"
 
 
-def test_bf16_wide_matches_large_kernel_full_n():
-    """The 32-query-wave kernel (no bias) against the 16-query-wave kernel (reached with an
+def test_bf16_tile32_matches_large_kernel_full_n():
+    """The 32-query-tile kernel (no bias) against the 16-query-wave kernel (reached with an
     all-zero bias, the same mathematics) at c5's N and H, every walker's count different:
     both are bf16 products with fp32 softmax, so they agree to bf16 rounding."""
     from hamiltonzero_amd import kernels
 
-    _say("bf16 wide vs large N=1024 H=16")
+    _say("bf16 32-query tiles vs 16-query kernel N=1024 H=16")
     B, N, H, D, T = 3, 1024, 16, 64, 2
     g = torch.Generator(device="cuda").manual_seed(11)
     r = lambda *s, sc=1.0: (torch.randn(*s, generator=g, device="cuda") * sc).to(torch.bfloat16)
@@ -367,7 +367,7 @@ def test_bf16_wide_matches_large_kernel_full_n():
                                                                                   device="cuda"))
     torch.cuda.synchronize()
     assert rel(host(o1), host(o2)) <= BF16_TOL
-    assert rel(host(l1), host(l2)) <= 1e-3  # the wide kernel normalises by its rounded weights
+    assert rel(host(l1), host(l2)) <= 1e-3  # the 32-query-tile kernel normalises by its rounded weights
     for t in range(T):
         assert rel(host(t1)[t], host(t2)[t]) <= BF16_TOL, f"tangent {t}"
     m = mask.cpu().numpy()
