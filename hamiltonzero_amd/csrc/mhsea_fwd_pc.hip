@@ -65,6 +65,20 @@ struct PcShape {
 // (the rows that eight lanes of a K read touch together) and flips bit 2 between rows
 // 4m and 4m+1, 4m+2 and 4m+3 (the row pairs of a V read), so neither read pattern
 // conflicts on the 32 LDS banks for D >= 32.
+// Row staging of the bias (mode 2 below): a consumer wave loads its 16 query rows whole and
+// gathers its keys from them through LDS, one region per tensor (e, e_t[t]). Row cq of a
+// region sits at cq * kERowF floats (64 keys and a pad that keeps rows 16-byte aligned).
+// Served where two workgroups per CU still fit (D = 8; D = 16 with T <= 1; D = 32 with
+// T = 0); sharing one region between the tensors costs more than it saves (measured at
+// D = 32, T = 1: 139 against 137 us).
+template <int D, int T>
+struct PcEStage {
+  static constexpr int kERowF = 68;
+  static constexpr int kRegion = 16 * kERowF * 4;
+  static constexpr int BYTES = 3 * (1 + T) * kRegion;  // three consumer waves
+  static constexpr bool OK = PcShape<D, T>::LDS + BYTES <= 80 * 1024;
+};
+
 template <int D>
 __device__ __forceinline__ int swz(int r) {
   return ((((r >> 2) & 3) | ((r & 1) << 2))) & (PcShape<D, 0>::CHUNKS - 1);
@@ -446,10 +460,16 @@ struct GateRegs {
 // layout [B, N, H/2, D]): ROLE 1, the gate head g, leaves sigma(g) and sigma'(g) gdot in gr
 // and writes nothing; ROLE 2, the value head v of the same pair, writes
 // y = sigma(g) v, ydot = sigma'(g) gdot v + sigma(g) vdot.
-template <int D, int T, bool GIVEN_LSE, bool HAS_E, int NJ, int ROLE, class PF, class SQ>
+// Bias mode EM: 0 none; 1 one 4-byte load per score (any layout of e); 2 the tile's query
+// rows loaded whole (a query's keys contiguous, 16-byte-aligned rows) and gathered through
+// the wave's LDS regions at estage.
+template <int D, int T, bool GIVEN_LSE, int EM, int NJ, int ROLE, class PF, class SQ>
 __device__ __forceinline__ void pc_tile(const FwdParams& p, const char* buf, const int16_t* slot_perm,
-                                        const QSet<D, T>& qs, int tile, PF&& pf, SQ&& sq, GateRegs<D, T>& gr) {
+                                        const QSet<D, T>& qs, int tile, PF&& pf, SQ&& sq, GateRegs<D, T>& gr,
+                                        float* estage) {
   using Sh = PcShape<D, T>;
+  constexpr bool HAS_E = EM != 0;
+  constexpr bool ROWS = EM == 2;
   constexpr int DG = Sh::DG, DT = Sh::DT, TT = Sh::TT;
   const int lane = threadIdx.x & 63;
   const int g = lane >> 4, c = lane & 15;
@@ -466,29 +486,44 @@ __device__ __forceinline__ void pc_tile(const FwdParams& p, const char* buf, con
   // ---- bias (and its tangents) for this lane's 4 NJ scores: issued first -------------
   float ev[NJ][4];
   float etv[TT][NJ][4];
+  float4 erow[ROWS ? T + 1 : 1][4];
   if constexpr (HAS_E) {
     const int64_t wstride = static_cast<int64_t>(N) * N * H;
     const int64_t ebytes = wstride * 4;
     const __amdgpu_buffer_rsrc_t e_rs = make_rsrc(
         p.e != nullptr ? static_cast<const float*>(p.e) + b * wstride : nullptr, p.e != nullptr ? ebytes : 0);
-    const int e_row = static_cast<int>(qsite * p.e_sq + h * p.e_sh);
+    auto et_rsrc = [&](int t) {
+      return make_rsrc(p.et != nullptr ? static_cast<const float*>(p.et) + t * p.et_stride + b * wstride : nullptr,
+                       p.et != nullptr ? ebytes : 0);
+    };
     const int e_oob = static_cast<int>(ebytes);
+    if constexpr (ROWS) {
+      // load i: rows 4i + g of the tile (query tile*16 + 4i + g), the lane's 16-byte chunk c
+      // (keys 4c..4c+3); rows of queries past the item's last are not read
 #pragma unroll
-    for (int jt = 0; jt < NJ; ++jt)
+      for (int i = 0; i < 4; ++i) {
+        const int cq = 4 * i + g;
+        const int qs_i = __shfl(qsite, cq, 64);
+        const bool ok = tile * 16 + cq < nq && 4 * c < N;
+        const int off = ok ? static_cast<int>((qs_i * p.e_sq + h * p.e_sh) * 4) + 16 * c : e_oob;
+        erow[0][i] = buf_load4(e_rs, off);
 #pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const int j = jt * 16 + 4 * r + g;
-        const int ks = key_all ? j : static_cast<int>(slot_perm[j & 63]);
-        const int eo = (j < nk && qvalid) ? (e_row + ks * static_cast<int>(p.e_sk)) * 4 : e_oob;
-        ev[jt][r] = buf_load1(e_rs, eo);
-#pragma unroll
-        for (int t = 0; t < T; ++t) {
-          const __amdgpu_buffer_rsrc_t et_rs =
-              make_rsrc(p.et != nullptr ? static_cast<const float*>(p.et) + t * p.et_stride + b * wstride : nullptr,
-                        p.et != nullptr ? ebytes : 0);
-          etv[t][jt][r] = buf_load1(et_rs, eo);
-        }
+        for (int t = 0; t < T; ++t) erow[1 + t][i] = buf_load4(et_rsrc(t), off);
       }
+    } else {
+      const int e_row = static_cast<int>(qsite * p.e_sq + h * p.e_sh);
+#pragma unroll
+      for (int jt = 0; jt < NJ; ++jt)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int j = jt * 16 + 4 * r + g;
+          const int ks = key_all ? j : static_cast<int>(slot_perm[j & 63]);
+          const int eo = (j < nk && qvalid) ? (e_row + ks * static_cast<int>(p.e_sk)) * 4 : e_oob;
+          ev[jt][r] = buf_load1(e_rs, eo);
+#pragma unroll
+          for (int t = 0; t < T; ++t) etv[t][jt][r] = buf_load1(et_rsrc(t), eo);
+        }
+    }
   }
   static_assert(ROLE == 0 || !GIVEN_LSE, "the gated collapse computes the forward");
   pf();
@@ -580,6 +615,16 @@ __device__ __forceinline__ void pc_tile(const FwdParams& p, const char* buf, con
       for (int jt = 0; jt < NJ; ++jt) ds[t][jt] = mfma16x4(kv[jt][s], qtf[t][s], ds[t][jt]);
   }
 
+  // ---- row-staged bias: the rows go to LDS while the matrix cores work on S -----------
+  constexpr int kRF = PcEStage<D, T>::kERowF;
+  if constexpr (ROWS) {
+#pragma unroll
+    for (int x = 0; x <= T; ++x)
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+        *reinterpret_cast<float4*>(estage + (x * 16 + 4 * i + g) * kRF + 4 * c) = erow[x][i];
+  }
+
   // ---- V and Vt rows for the products, read while the matrix cores finish S -----------
   const bool colok = D % 16 == 0 || c < D;
   const int vcol = (D % 16 == 0) ? c : min(c, D - 1);
@@ -598,6 +643,27 @@ __device__ __forceinline__ void pc_tile(const FwdParams& p, const char* buf, con
         for (int t = 0; t < T; ++t) vta[jt][t][r][dt] = *reinterpret_cast<const float*>(V0 + (1 + t) * Sh::TILE + off);
       }
   compiler_fence();
+
+  // ---- row-staged bias: this lane's keys from the staged rows (the wave reads only what
+  // it wrote, and its LDS accesses complete in order) ----------------------------------
+  if constexpr (ROWS) {
+#pragma unroll
+    for (int x = 0; x <= T; ++x) {
+      const float* const rg = estage + x * 16 * kRF;
+#pragma unroll
+      for (int jt = 0; jt < NJ; ++jt)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int j = jt * 16 + 4 * r + g;
+          const int ks = key_all ? j : static_cast<int>(slot_perm[j & 63]);
+          const float val = rg[c * kRF + ks];
+          if (x == 0)
+            ev[jt][r] = val;
+          else
+            etv[x - 1][jt][r] = val;
+        }
+    }
+  }
 
   // ---- bias, validity (only the last key tile can hold padding), max ----------------
   float mx = -INFINITY;
@@ -773,10 +839,13 @@ __device__ __forceinline__ void pc_tile(const FwdParams& p, const char* buf, con
   }
 }
 
-template <int D, int T, bool GIVEN_LSE, bool HAS_E, bool GATED>
-__device__ __forceinline__ void pc_consumer(const FwdParams& p, const char* lds, const ItemSeq& seq, int cnt) {
+template <int D, int T, bool GIVEN_LSE, int EM, bool GATED>
+__device__ __forceinline__ void pc_consumer(const FwdParams& p, char* lds, const ItemSeq& seq, int cnt) {
   using Sh = PcShape<D, T>;
   const int wave = threadIdx.x >> 6;
+  float* const estage = EM == 2 ? reinterpret_cast<float*>(lds + 2 * Sh::BUF + kSlots * kSlotBytes) +
+                                      wave * (1 + T) * (PcEStage<D, T>::kRegion / 4)
+                                : nullptr;
   const int N = p.N;
   const bool km = p.key_mask != 0;
   const char* const slots = lds + 2 * Sh::BUF;
@@ -809,10 +878,10 @@ __device__ __forceinline__ void pc_consumer(const FwdParams& p, const char* lds,
     const int16_t* sp = slot_perm(k);
     if (wave * 16 < nq) {
       switch ((nk + 15) >> 4) {
-        case 1: pc_tile<D, T, GIVEN_LSE, HAS_E, 1, R>(p, buf, sp, qs, wave, pf, sq, gm); break;
-        case 2: pc_tile<D, T, GIVEN_LSE, HAS_E, 2, R>(p, buf, sp, qs, wave, pf, sq, gm); break;
-        case 3: pc_tile<D, T, GIVEN_LSE, HAS_E, 3, R>(p, buf, sp, qs, wave, pf, sq, gm); break;
-        default: pc_tile<D, T, GIVEN_LSE, HAS_E, 4, R>(p, buf, sp, qs, wave, pf, sq, gm); break;
+        case 1: pc_tile<D, T, GIVEN_LSE, EM, 1, R>(p, buf, sp, qs, wave, pf, sq, gm, estage); break;
+        case 2: pc_tile<D, T, GIVEN_LSE, EM, 2, R>(p, buf, sp, qs, wave, pf, sq, gm, estage); break;
+        case 3: pc_tile<D, T, GIVEN_LSE, EM, 3, R>(p, buf, sp, qs, wave, pf, sq, gm, estage); break;
+        default: pc_tile<D, T, GIVEN_LSE, EM, 4, R>(p, buf, sp, qs, wave, pf, sq, gm, estage); break;
       }
     } else {
       pf();
@@ -824,10 +893,10 @@ __device__ __forceinline__ void pc_consumer(const FwdParams& p, const char* lds,
       QSet<D, T> q3;
       pc_load_q<D, T, GIVEN_LSE>(p, q3, qs.b, qs.h, qs.n_phys, sp, 3);
       switch ((nk + 15) >> 4) {
-        case 1: pc_tile<D, T, GIVEN_LSE, HAS_E, 1, R>(p, buf, sp, q3, 3, [] {}, [] {}, gx); break;
-        case 2: pc_tile<D, T, GIVEN_LSE, HAS_E, 2, R>(p, buf, sp, q3, 3, [] {}, [] {}, gx); break;
-        case 3: pc_tile<D, T, GIVEN_LSE, HAS_E, 3, R>(p, buf, sp, q3, 3, [] {}, [] {}, gx); break;
-        default: pc_tile<D, T, GIVEN_LSE, HAS_E, 4, R>(p, buf, sp, q3, 3, [] {}, [] {}, gx); break;
+        case 1: pc_tile<D, T, GIVEN_LSE, EM, 1, R>(p, buf, sp, q3, 3, [] {}, [] {}, gx, estage); break;
+        case 2: pc_tile<D, T, GIVEN_LSE, EM, 2, R>(p, buf, sp, q3, 3, [] {}, [] {}, gx, estage); break;
+        case 3: pc_tile<D, T, GIVEN_LSE, EM, 3, R>(p, buf, sp, q3, 3, [] {}, [] {}, gx, estage); break;
+        default: pc_tile<D, T, GIVEN_LSE, EM, 4, R>(p, buf, sp, q3, 3, [] {}, [] {}, gx, estage); break;
       }
     }
     __builtin_amdgcn_s_waitcnt(kWaitLgkm0);
@@ -850,7 +919,7 @@ __device__ __forceinline__ void pc_consumer(const FwdParams& p, const char* lds,
   }
 }
 
-template <int D, int T, bool GIVEN_LSE, bool HAS_E, bool GATED>
+template <int D, int T, bool GIVEN_LSE, int EM, bool GATED>
 __global__ void __launch_bounds__(256, 2) mhsea_fwd_pc_kernel(const FwdParams p) {
   using Sh = PcShape<D, T>;
   extern __shared__ float4 smem4[];
@@ -865,15 +934,16 @@ __global__ void __launch_bounds__(256, 2) mhsea_fwd_pc_kernel(const FwdParams p)
   if ((threadIdx.x >> 6) == kProducerWave)
     pc_producer<D, T, GIVEN_LSE, GATED>(p, lds, seq, cnt);
   else
-    pc_consumer<D, T, GIVEN_LSE, HAS_E, GATED>(p, lds, seq, cnt);
+    pc_consumer<D, T, GIVEN_LSE, EM, GATED>(p, lds, seq, cnt);
   (void)Sh::LDS;
 }
 
-template <int D, int T, bool GIVEN_LSE, bool HAS_E, bool GATED>
+template <int D, int T, bool GIVEN_LSE, int EM, bool GATED>
 hipError_t launch_pc_t(const FwdParams& p, hipStream_t stream) {
   using Sh = PcShape<D, T>;
-  auto kern = mhsea_fwd_pc_kernel<D, T, GIVEN_LSE, HAS_E, GATED>;
-  const size_t lds = Sh::LDS;
+  static_assert(EM != 2 || PcEStage<D, T>::OK, "two workgroups per CU");
+  auto kern = mhsea_fwd_pc_kernel<D, T, GIVEN_LSE, EM, GATED>;
+  const size_t lds = Sh::LDS + (EM == 2 ? PcEStage<D, T>::BYTES : 0);
   if (lds > 64 * 1024) {
     hipError_t err = hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
                                          hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(lds));
@@ -906,17 +976,32 @@ constexpr bool pc_shape_ok() {
   return PcShape<D, T>::LDS <= 80 * 1024;
 }
 
+// Bias rows can be staged whole when a query's keys are contiguous and every row starts on a
+// 16-byte boundary (the [B, N, H, N] layout with N a multiple of 4, aligned base pointers).
+bool e_rows_ok(const FwdParams& p) {
+  auto aligned = [](const void* x) { return (reinterpret_cast<uintptr_t>(x) & 15) == 0; };
+  return p.e_sk == 1 && p.e_sq % 4 == 0 && p.e_sh % 4 == 0 && p.N % 4 == 0 && p.et_stride % 4 == 0 &&
+         aligned(p.e) && aligned(p.et);
+}
+
+template <int D, int T, bool GIVEN_LSE, bool GATED>
+hipError_t launch_pc_em(const FwdParams& p, hipStream_t stream) {
+  if (p.e == nullptr && p.et == nullptr) return launch_pc_t<D, T, GIVEN_LSE, 0, GATED>(p, stream);
+  if constexpr (PcEStage<D, T>::OK) {
+    if (e_rows_ok(p)) return launch_pc_t<D, T, GIVEN_LSE, 2, GATED>(p, stream);
+  }
+  return launch_pc_t<D, T, GIVEN_LSE, 1, GATED>(p, stream);
+}
+
 template <int D, int T, bool GIVEN_LSE>
 hipError_t dispatch_e(const FwdParams& p, hipStream_t stream) {
   if constexpr (pc_shape_ok<D, T>()) {
-    const bool e = p.e != nullptr || p.et != nullptr;
     if constexpr (!GIVEN_LSE) {
-      if (p.gated) return e ? launch_pc_t<D, T, false, true, true>(p, stream) : launch_pc_t<D, T, false, false, true>(p, stream);
+      if (p.gated) return launch_pc_em<D, T, false, true>(p, stream);
     } else {
       if (p.gated) return hipErrorInvalidValue;
     }
-    if (e) return launch_pc_t<D, T, GIVEN_LSE, true, false>(p, stream);
-    return launch_pc_t<D, T, GIVEN_LSE, false, false>(p, stream);
+    return launch_pc_em<D, T, GIVEN_LSE, false>(p, stream);
   }
   return hipErrorInvalidValue;
 }

@@ -162,12 +162,15 @@ def test_bwd_at_item_counts(case):
         assert rel(got[nm][idx], ref[nm], floors[nm]) <= tol, nm
 
 
-def test_gated_at_item_counts():
-    """The gated collapse at c2's full shape with per-walker scattered masks and bias."""
+@pytest.mark.parametrize("seed,H,D", [(131, 8, 32), (132, 32, 16)], ids=["c2_shape", "trunk_shape"])
+def test_gated_at_item_counts(seed, H, D):
+    """The gated collapse at full batch with per-walker scattered masks and bias: c2's shape
+    (bias read per score) and the trunk's [1024, 64, 32, 16] (bias rows staged through LDS,
+    16 head pairs per walker, 32 items per workgroup)."""
     from hamiltonzero_amd import kernels
 
-    _say("gated items c2 full")
-    a, d, tol = _case(131, 1024, 64, 8, 32, -1, scattered=True, with_e=True)
+    _say(f"gated items B=1024 H={H} D={D}")
+    a, d, tol = _case(seed, 1024, 64, H, D, -1, scattered=True, with_e=True)
     y, ty = kernels.mhsea_fwd_jvp_gated(d["q"], d["k"], d["v"], d["mask"], d["qt"], d["kt"], d["vt"], d["e"],
                                         d["et"])
     torch.cuda.synchronize()

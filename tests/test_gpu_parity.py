@@ -104,6 +104,13 @@ CASES = [
     ("n64_keymask_d16_t2", 4, 64, 2, 16, 40, True, False, "qhk", True, 1.0, 2, False),
     ("n40_d8_t2_bias", 3, 40, 2, 8, 25, True, True, "qkh", False, 0.5, 2, False),
     ("n64_mixed_counts", 24, 64, 3, 32, -1, True, True, "qhk", False, 1.0, 1, False),
+    # bias rows staged whole through LDS (keys contiguous, N a multiple of 4, D <= 16 with
+    # tangents), with the key mask, and N = 37, where rows are not 16-byte aligned and each
+    # score's bias is read on its own
+    ("n64_d16_rows_bias", 4, 64, 4, 16, 36, True, True, "qhk", False, 1.0, 1, False),
+    ("n44_d8_t2_rows_bias", 3, 44, 2, 8, 30, True, True, "qhk", False, 0.5, 2, False),
+    ("n60_d16_keymask_rows_bias", 3, 60, 2, 16, 20, True, True, "qhk", True, 1.0, 1, False),
+    ("n37_d16_unaligned_rows_bias", 3, 37, 2, 16, 25, True, True, "qhk", False, 1.0, 1, False),
     # float32 D = 64, N <= 64: one tangent (streaming kernel) and two (LDS-streaming kernel)
     ("n64_d64_t1_fp32", 3, 64, 2, 64, 48, False, False, "qhk", False, 1.0, 1, False),
     ("n64_d64_t2_fp32_bias", 3, 64, 2, 64, 48, True, True, "qkh", False, 0.5, 2, False),
@@ -238,6 +245,32 @@ def test_deterministic_bitwise():
     g2 = kernels.mhsea_bwd(d["q"], d["k"], d["v"], d["mask"], r1[1], r1[0], d["dout"], d["e"])
     for x, y in zip((*r1, *g1), (*r2, *g2)):
         assert torch.equal(x, y)
+
+
+def test_bias_row_staging_matches_per_score_loads():
+    """32 < N <= 64, float32: bias rows of the [B, N, H, N] layout (a query's keys contiguous)
+    are staged whole and gathered through LDS; the [B, N, N, H] layout is read one score at
+    a time. The same values in either layout add the same floats in the same order, so the
+    outputs are bit-identical, plain and gated (and the staged path matches the oracle)."""
+    from hamiltonzero_amd import kernels
+
+    _say("bias rows staged vs per-score loads")
+    a = make_inputs(55, 6, 64, 4, 16, 36, scattered=True, with_e=True, e_layout="qhk", T=1)
+    d = {n: to_dev(x, torch.float32) for n, x in a.items()}
+    e2 = d["e"].permute(0, 1, 3, 2).contiguous()  # [B, N, N, H]
+    et2 = d["et"].permute(0, 1, 2, 4, 3).contiguous()
+    args = (d["q"], d["k"], d["v"], d["mask"], d["qt"], d["kt"], d["vt"])
+    staged = kernels.mhsea_fwd_jvp(*args, d["e"], d["et"])
+    single = kernels.mhsea_fwd_jvp(*args, e2, et2, e_layout="qkh")
+    gs = kernels.mhsea_fwd_jvp_gated(*args, e=d["e"], et=d["et"])
+    g1 = kernels.mhsea_fwd_jvp_gated(*args, e=e2, et=et2, e_layout="qkh")
+    torch.cuda.synchronize()
+    for x, y in zip((*staged, *gs), (*single, *g1)):
+        assert torch.equal(x, y)
+    ref_out, _ = O.fwd(a["q"], a["k"], a["e"], a["v"], a["mask"])
+    ref_t = O.jvp(a["q"], a["k"], a["e"], a["v"], a["mask"], a["qt"][0], a["kt"][0], a["et"][0], a["vt"][0])
+    assert rel(host(staged[0]), ref_out) <= F32_TOL
+    assert rel(host(staged[2])[0], ref_t) <= F32_TOL
 
 
 @pytest.mark.parametrize("bf16", [False, True], ids=["f32", "bf16"])
