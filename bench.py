@@ -579,8 +579,11 @@ def run_executor(args, cfg):
 
 def run_trunk(args, cfg):
     """Bench leg of the trunk attention with its produced bias: hz_pair_bias (edge, edge_t ->
-    e, e_t in the attention layout) then hz_mhsea_fwd_jvp_gated. Config: B, N, H (kernel
-    heads), D (d_head), n_phys, T = 1; edge channels 96, bias hidden 64."""
+    e, e_t in the attention layout), hz_mhsea_fwd_jvp_gated, then W_O (hz_gated_out_proj).
+    Config: B, N, H (kernel heads), D (d_head), n_phys, T = 1; edge channels 96, bias hidden
+    64. W_O receives the site mask: the gated attention writes the masked sites' rows of y as
+    exact zeros and W_O has no bias (trunk.py:54), so the masked product, which skips those
+    rows, equals the reference's unmasked W_O."""
     import torch
 
     from hamiltonzero_amd import _native
@@ -627,8 +630,8 @@ def run_trunk(args, cfg):
                                                  H, D, 1.0, 0))
 
     def project(i):
-        _native.check(lib.hz_gated_out_proj(s, P(d["y"]), P(d["ty"]), P(w_o), None, P(d["delta"]), P(d["delta_t"]),
-                                            B, N, d_attn, d_e, 1))
+        _native.check(lib.hz_gated_out_proj(s, P(d["y"]), P(d["ty"]), P(w_o), P(mask), P(d["delta"]),
+                                            P(d["delta_t"]), B, N, d_attn, d_e, 1))
 
     def step(i):
         produce(i)

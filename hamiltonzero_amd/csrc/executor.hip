@@ -19,6 +19,7 @@
 #include <hip/hip_runtime.h>
 
 #include <mutex>
+#include <type_traits>
 
 #include "mhsea_device.h"
 #include "mhsea_launch.h"
@@ -240,6 +241,168 @@ gemm_f32_kernel(const float* __restrict__ A, const float* __restrict__ Bm, float
     }
 }
 
+// Site-masked product C[m, :] = mask[m] != 0 ? A[m, :] B : 0 with the masked rows skipped.
+// A workgroup takes kRM rows of A and one 128-column tile of C: its physical rows (in order)
+// are compacted into the LDS tile, so only ceil(n / 16) row blocks are multiplied, and its
+// masked rows of C are written as zeros. Wave w owns columns [32 w, 32 w + 32) of the tile for
+// every row block. Workgroups are numbered so that the column tiles of one row block run on
+// one XCD (one L2 holds their A rows). K and N are multiples of 4 (16-byte staging loads).
+constexpr int kRM = 256;
+constexpr int kRMPad = kRM + 16;
+constexpr int kRMBlocks = kRM / 16;
+
+__global__ void __launch_bounds__(256, 2)
+gemm_rows_f32_kernel(const float* __restrict__ A, const float* __restrict__ Bm, float* __restrict__ C,
+                     const uint8_t* __restrict__ mask, int64_t M, int N, int K, int ncol) {
+  __shared__ float As[2][kBK][kRMPad];
+  __shared__ float Bs[2][kBK][kBPad];
+  __shared__ int16_t prow[kRM], mrow[kRM];
+  __shared__ int counts[8];
+  const int tid = threadIdx.x;
+  const int lane = tid & 63, wave = tid >> 6;
+  const int g = lane >> 4, c = lane & 15;
+  const int64_t L = xcd_logical_block(blockIdx.x, gridDim.x);
+  const int64_t m0 = (L / ncol) * kRM;
+  const int n0 = static_cast<int>(L % ncol) * kBN;
+  const int wn = wave * 32;
+
+  // ---- this workgroup's physical and masked rows, each list in ascending order ---------
+  const bool valid = m0 + tid < M;
+  const bool phys = valid && mask[m0 + tid] != 0;
+  const uint64_t pb = __ballot(phys), mb = __ballot(valid && !phys);
+  const uint64_t below = (uint64_t(1) << lane) - 1;
+  if (lane == 0) {
+    counts[wave] = __popcll(pb);
+    counts[4 + wave] = __popcll(mb);
+  }
+  __syncthreads();
+  int pbase = 0, mbase = 0;
+#pragma unroll
+  for (int w = 0; w < 4; ++w) {
+    pbase += w < wave ? counts[w] : 0;
+    mbase += w < wave ? counts[4 + w] : 0;
+  }
+  const int n = counts[0] + counts[1] + counts[2] + counts[3];
+  const int nm = counts[4] + counts[5] + counts[6] + counts[7];
+  if (phys) prow[pbase + __popcll(pb & below)] = static_cast<int16_t>(tid);
+  if (valid && !phys) mrow[mbase + __popcll(mb & below)] = static_cast<int16_t>(tid);
+  __syncthreads();
+
+  // masked rows of this column tile: zeros, 16 bytes per store
+  for (int i = tid; i < nm * (kBN / 4); i += 256) {
+    const int col = n0 + 4 * (i % (kBN / 4));
+    if (col < N)
+      *reinterpret_cast<float4*>(C + (m0 + mrow[i / (kBN / 4)]) * N + col) = make_float4(0.f, 0.f, 0.f, 0.f);
+  }
+  if (n == 0) return;  // workgroup-uniform
+
+  // global -> register staging: A slots 256 x 16 as 1024 float4 (slot = it / 4, k4 = it % 4;
+  // slots past n stay zero; each slot's row offset is fixed for the whole K loop), B tile
+  // 16 x 128 as 512 float4 (k = it / 32, n4 = it % 32)
+  int64_t aoff[4];
+#pragma unroll
+  for (int u = 0; u < 4; ++u) {
+    const int slot = (tid + 256 * u) >> 2;
+    aoff[u] = slot < n ? (m0 + prow[slot]) * K : -1;
+  }
+  float4 ra[4], rb[2];
+  auto gload = [&](int k0) {
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const int kk = k0 + 4 * ((tid + 256 * u) & 3);
+      ra[u] = make_float4(0.f, 0.f, 0.f, 0.f);
+      if (aoff[u] >= 0 && kk < K) ra[u] = *reinterpret_cast<const float4*>(A + aoff[u] + kk);
+    }
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+      const int it = tid + 256 * u;
+      const int kb = k0 + (it >> 5);
+      const int nn = n0 + 4 * (it & 31);
+      rb[u] = (kb < K && nn < N) ? *reinterpret_cast<const float4*>(Bm + static_cast<int64_t>(kb) * N + nn)
+                                 : make_float4(0.f, 0.f, 0.f, 0.f);
+    }
+  };
+  auto sstore = [&](int buf) {
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const int it = tid + 256 * u;
+      const int r = it >> 2, k4 = 4 * (it & 3);
+      const int rs = r ^ (16 * ((k4 >> 2) & 3));  // as in gemm_f32_kernel
+      As[buf][k4 + 0][rs] = ra[u].x;
+      As[buf][k4 + 1][rs] = ra[u].y;
+      As[buf][k4 + 2][rs] = ra[u].z;
+      As[buf][k4 + 3][rs] = ra[u].w;
+    }
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+      const int it = tid + 256 * u;
+      *reinterpret_cast<float4*>(&Bs[buf][it >> 5][4 * (it & 31)]) = rb[u];
+    }
+  };
+
+  // the K loop and the stores for NMT = ceil(n / 16) row blocks, a compile-time count so
+  // the products run without branches
+  auto body = [&](auto nmt_c) {
+    constexpr int NMT = decltype(nmt_c)::value;
+    v4f acc[NMT][2];
+#pragma unroll
+    for (int mt = 0; mt < NMT; ++mt) acc[mt][0] = acc[mt][1] = zero4();
+    const int nk = (K + kBK - 1) / kBK;
+    gload(0);
+    sstore(0);
+    __syncthreads();
+    for (int kt = 0; kt < nk; ++kt) {
+      const int buf = kt & 1;
+      if (kt + 1 < nk) gload((kt + 1) * kBK);
+#pragma unroll
+      for (int ks = 0; ks < kBK; ks += 4) {
+        const float b0 = Bs[buf][ks + g][wn + c];
+        const float b1 = Bs[buf][ks + g][wn + 16 + c];
+#pragma unroll
+        for (int mt = 0; mt < NMT; ++mt) {
+          const float af = As[buf][ks + g][(16 * mt + c) ^ (16 * ((ks >> 2) & 3))];
+          acc[mt][0] = mfma16x4(af, b0, acc[mt][0]);
+          acc[mt][1] = mfma16x4(af, b1, acc[mt][1]);
+        }
+      }
+      if (kt + 1 < nk) sstore(buf ^ 1);
+      __syncthreads();
+    }
+    // lane (g, c) holds C[prow[16 mt + 4 g + r]][n0 + wn + 16 nt + c]
+#pragma unroll
+    for (int mt = 0; mt < NMT; ++mt)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int slot = 16 * mt + 4 * g + r;
+        const int64_t row = m0 + prow[slot < n ? slot : 0];
+#pragma unroll
+        for (int nt = 0; nt < 2; ++nt) {
+          const int col = n0 + wn + 16 * nt + c;
+          if (slot < n && col < N) C[row * N + col] = acc[mt][nt][r];
+        }
+      }
+  };
+  using std::integral_constant;
+  switch ((n + 15) >> 4) {
+    case 1: body(integral_constant<int, 1>{}); break;
+    case 2: body(integral_constant<int, 2>{}); break;
+    case 3: body(integral_constant<int, 3>{}); break;
+    case 4: body(integral_constant<int, 4>{}); break;
+    case 5: body(integral_constant<int, 5>{}); break;
+    case 6: body(integral_constant<int, 6>{}); break;
+    case 7: body(integral_constant<int, 7>{}); break;
+    case 8: body(integral_constant<int, 8>{}); break;
+    case 9: body(integral_constant<int, 9>{}); break;
+    case 10: body(integral_constant<int, 10>{}); break;
+    case 11: body(integral_constant<int, 11>{}); break;
+    case 12: body(integral_constant<int, 12>{}); break;
+    case 13: body(integral_constant<int, 13>{}); break;
+    case 14: body(integral_constant<int, 14>{}); break;
+    case 15: body(integral_constant<int, 15>{}); break;
+    default: body(integral_constant<int, 16>{}); break;
+  }
+}
+
 template <int EPI>
 hipError_t launch_gemm(const float* A, const float* B, float* C, const float* aux, int64_t M, int N, int K,
                        int h_rows, int64_t row0, hipStream_t stream) {
@@ -458,6 +621,14 @@ hipError_t launch_factorized_apply(const float* x, const float* V, const float* 
 
 hipError_t launch_out_proj(const float* y, const float* w_o, const uint8_t* mask, float* delta, int64_t M, int d_in,
                            int d_out, hipStream_t stream) {
+  if (mask != nullptr && d_out % 4 == 0 && d_in % 4 == 0) {
+    const int64_t ncol = (d_out + kBN - 1) / kBN;
+    const int64_t blocks = ncol * ((M + kRM - 1) / kRM);
+    if (blocks > 0x7fffffffLL) return hipErrorInvalidValue;
+    hipLaunchKernelGGL(gemm_rows_f32_kernel, dim3(static_cast<unsigned>(blocks)), dim3(256), 0, stream, y, w_o, delta,
+                       mask, M, d_out, d_in, static_cast<int>(ncol));
+    return hipGetLastError();
+  }
   if (mask != nullptr)
     return launch_gemm<kEpiRowMask>(y, w_o, delta, reinterpret_cast<const float*>(mask), M, d_out, d_in, 1, 0, stream);
   return launch_gemm<kEpiPlain>(y, w_o, delta, nullptr, M, d_out, d_in, 1, 0, stream);

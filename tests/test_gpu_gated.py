@@ -160,7 +160,7 @@ def test_gated_edge_attention_autograd(with_e):
 
 
 @pytest.mark.parametrize("T,masked,shape", [(0, False, (3, 17, 2, 8, 5)), (1, True, (64, 64, 16, 16, 512)),
-                                            (2, True, (5, 33, 3, 8, 70))])
+                                            (2, True, (5, 33, 3, 8, 70)), (1, True, (7, 37, 4, 16, 132))])
 def test_gated_out_proj(T, masked, shape):
     """W_O after the collapse (trunk.py:138-144), with the tree's site mask
     (tree.py:1479-1488) and the tangents, against the float64 oracle."""
@@ -181,6 +181,31 @@ def test_gated_out_proj(T, masked, shape):
         assert np.all(delta.cpu().numpy()[~mask] == 0.0)
     for t in range(T):
         assert rel(dt[t].cpu().numpy(), O.out_proj(ty[t], w, mask)) <= TOL
+
+
+def test_out_proj_masked_row_compaction():
+    """The masked projection compacts each workgroup's physical rows (256 rows per workgroup):
+    workgroups with every row masked, every row physical, one physical row, and a partial
+    last workgroup, against the float64 oracle; masked rows are exact zeros."""
+    from hamiltonzero_amd import kernels
+
+    _say("out proj row compaction")
+    B, N, hh, D, d_e = 13, 64, 16, 16, 512  # M = 832: three full workgroups and one of 64 rows
+    rng = np.random.default_rng(7)
+    y = rng.standard_normal((B, N, hh, D), dtype=np.float32)
+    ty = rng.standard_normal((1, B, N, hh, D), dtype=np.float32)
+    w = (rng.standard_normal((hh * D, d_e)) / np.sqrt(hh * D)).astype(np.float32)
+    flat = np.zeros(B * N, dtype=bool)
+    flat[256:512] = True              # workgroup 1: every row physical
+    flat[512 + 77] = True             # workgroup 2: one physical row
+    flat[768:] = rng.random(64) < 0.5  # workgroup 3 (partial): scattered
+    mask = flat.reshape(B, N)         # workgroup 0: every row masked
+    dev = lambda x: torch.from_numpy(np.ascontiguousarray(x)).cuda()  # noqa: E731
+    delta, dt = kernels.gated_out_proj(dev(y), dev(w), ty=dev(ty), mask=dev(mask))
+    torch.cuda.synchronize()
+    assert rel(delta.cpu().numpy(), O.out_proj(y, w, mask)) <= TOL
+    assert rel(dt[0].cpu().numpy(), O.out_proj(ty[0], w, mask)) <= TOL
+    assert np.all(delta.cpu().numpy()[~mask] == 0.0) and np.all(dt[0].cpu().numpy()[~mask] == 0.0)
 
 
 def test_gated_then_out_proj_at_the_trunk_shape():
