@@ -160,7 +160,8 @@ def test_gated_edge_attention_autograd(with_e):
 
 
 @pytest.mark.parametrize("T,masked,shape", [(0, False, (3, 17, 2, 8, 5)), (1, True, (64, 64, 16, 16, 512)),
-                                            (2, True, (5, 33, 3, 8, 70)), (1, True, (7, 37, 4, 16, 132))])
+                                            (2, True, (5, 33, 3, 8, 70)), (1, True, (7, 37, 4, 16, 132)),
+                                            (1, True, (3, 40, 3, 4, 20))])
 def test_gated_out_proj(T, masked, shape):
     """W_O after the collapse (trunk.py:138-144), with the tree's site mask
     (tree.py:1479-1488) and the tangents, against the float64 oracle."""
