@@ -170,7 +170,10 @@ int hz_mhsea_fwd_jvp_gated(hipStream_t stream,
  *     delta_t[t, b, i]  = (ty[t, b, i, :] W_o) * (mask[b, i] != 0)
  * y [B, N, d_attn] is hz_mhsea_fwd_jvp_gated's y [B, N, H/2, D] read as rows (d_attn =
  * H/2 * D), ty [T, B, N, d_attn]; W_o [d_attn, d_e] (BiasFreeLinear, [in, out]); float32,
- * fp32 matrix cores. T in [0, 3].
+ * fp32 matrix cores. T in [0, 3]. With a mask (d_attn and d_e multiples of 4), rows with
+ * mask 0 are written as zeros without being read or multiplied, so only the physical rows
+ * cost matrix work; they equal the formula above for finite y (a NaN or Inf in a masked row
+ * of y does not reach delta).
  */
 int hz_gated_out_proj(hipStream_t stream, const float* y, const float* ty, const float* w_o, const uint8_t* mask,
                       float* delta, float* delta_t, int64_t B, int64_t N, int64_t d_attn, int64_t d_e, int64_t T);
