@@ -284,7 +284,9 @@ def gated_out_proj(y: Tensor, w_o: Tensor, ty: Optional[Tensor] = None,
     w_o`` (the trunk's ``W_O``, ``trunk.py:138-144``), times the site mask when ``mask`` is
     given (the tree's ``mask_q * (out_flat @ w_o)``, ``tree.py:1479-1488``), and the same for
     each tangent row ``ty [T, ...]`` (or a single ``[...]`` direction). ``y`` is ``[B, N,
-    H/2, D]`` (``mhsea_fwd_jvp_gated``'s output) or ``[B, N, d_attn]``; float32 CUDA tensors."""
+    H/2, D]`` (``mhsea_fwd_jvp_gated``'s output) or ``[B, N, d_attn]``; float32 CUDA tensors.
+    With a mask, rows of masked sites are written as zeros without being read (equal to the
+    product for finite ``y``), so only the physical rows cost matrix work."""
     if y.dim() not in (3, 4):
         raise ValueError(f"y must be [B, N, H/2, D] or [B, N, d_attn], got {tuple(y.shape)}")
     B, N = y.shape[0], y.shape[1]
