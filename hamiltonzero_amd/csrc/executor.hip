@@ -247,9 +247,8 @@ gemm_f32_kernel(const float* __restrict__ A, const float* __restrict__ Bm, float
 // masked rows of C are written as zeros. Wave w owns columns [32 w, 32 w + 32) of the tile for
 // every row block. Workgroups are numbered so that the column tiles of one row block run on
 // one XCD (one L2 holds their A rows). K and N are multiples of 4 (16-byte staging loads).
-constexpr int kRM = 256;
+constexpr int kRM = 256;  // 16 row blocks: the dispatch below instantiates 1..16
 constexpr int kRMPad = kRM + 16;
-constexpr int kRMBlocks = kRM / 16;
 
 __global__ void __launch_bounds__(256, 2)
 gemm_rows_f32_kernel(const float* __restrict__ A, const float* __restrict__ Bm, float* __restrict__ C,
