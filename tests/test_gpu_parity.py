@@ -273,29 +273,31 @@ def test_bias_row_staging_matches_per_score_loads():
     assert rel(host(staged[2])[0], ref_t) <= F32_TOL
 
 
+@pytest.mark.parametrize("layout", ["qkh", "qhk"])
 @pytest.mark.parametrize("bf16", [False, True], ids=["f32", "bf16"])
 @pytest.mark.parametrize("N,D", [(16, 32), (64, 16), (200, 64)])
-def test_keymask_no_physical_key_large_logits(N, D, bf16):
+def test_keymask_no_physical_key_large_logits(N, D, bf16, layout):
     """Key mask, no physical key, logits of a few hundred: the reference's float32 penalty
     rounds every logit to a multiple of 64 (pallas_attention.py:34-35), so the weights sit on
     the keys of the top multiple. The bias is 64 m + u with integer m in [-3, 3] and |u| <= 20,
     so every logit is at least 10 away from a rounding tie of fl32(s - 1e9). Every entry point
-    against the oracle, plus a walker with physical keys in the same batch."""
+    against the oracle, plus a walker with physical keys in the same batch; both bias layouts
+    (at N = 64 the [B, N, H, N] one takes the staged-row path of the forward)."""
     from hamiltonzero_amd import kernels
 
-    _say(f"keymask empty large logits N={N} D={D} bf16={bf16}")
+    _say(f"keymask empty large logits N={N} D={D} bf16={bf16} layout={layout}")
     B, H = 3, 2
     rng = np.random.default_rng(N + D)
-    a = make_inputs(int(rng.integers(1000)), B, N, H, D, 0, with_e=True, e_layout="qkh", T=2, bf16=bf16)
+    a = make_inputs(int(rng.integers(1000)), B, N, H, D, 0, with_e=True, e_layout=layout, T=2, bf16=bf16)
     a["mask"][1, : N // 2] = True  # walker 1 keeps physical keys
     e = 64.0 * rng.integers(-3, 4, size=a["e"].shape) + rng.uniform(-20.0, 20.0, size=a["e"].shape)
     a["e"] = torch.from_numpy(e.astype(np.float32)).bfloat16().float().numpy() if bf16 else e.astype(np.float32)
-    s = O._es("bihd,bjhd->bhij", a["q"].astype(np.float64), a["k"]) + O._e_bhqk(a["e"], "qkh")
+    s = O._es("bihd,bjhd->bhij", a["q"].astype(np.float64), a["k"]) + O._e_bhqk(a["e"], layout)
     assert np.abs(s).max() > 150.0
     assert np.min(np.abs((s - 32.0) / 64.0 - np.round((s - 32.0) / 64.0))) * 64.0 > 10.0
     dt = torch.bfloat16 if bf16 else torch.float32
     d = {n: to_dev(x, dt) for n, x in a.items()}
-    opts = dict(key_mask=True, e_layout="qkh", scale=1.0)
+    opts = dict(key_mask=True, e_layout=layout, scale=1.0)
     tol = BF16_TOL if bf16 else F32_TOL
     # Calls that read a stored float32 lse (the tangent from (out, lse), the backward) see P
     # with the relative error of lse's rounding, up to |lse| 2^-24 (~1.2e-5 at |lse| ~ 200,
