@@ -100,8 +100,15 @@ __device__ __forceinline__ void load_rows(const float* edge_b, const float* edge
   }
 }
 
+// Workgroups per CU: two while the staged weights and the wave lists fit half of the LDS
+// (every instantiation but C = 128 with 64 heads, whose weights take 83.5 KB), else one.
+template <int C, int HB>
+constexpr int pb_occupancy() {
+  return (PBLds<C, HB>::kFloats * 4 + kPBWaves * kPBListN * 2) <= 80 * 1024 ? 2 : 1;
+}
+
 template <int C, int HB, bool TAN>
-__global__ void __launch_bounds__(256, 2) pair_bias_kernel(PairBiasParams p) {
+__global__ void __launch_bounds__(256, (pb_occupancy<C, HB>())) pair_bias_kernel(PairBiasParams p) {
   using L = PBLds<C, HB>;
   constexpr int C4 = C / 4;    // channels per lane group = layer-1 K steps
   constexpr int CG = C / 16;   // float4 groups per lane group
@@ -364,7 +371,9 @@ __global__ void __launch_bounds__(256, 2) pair_bias_kernel(PairBiasParams p) {
 }
 
 template <int C, int HB>
-hipError_t launch_pb(const PairBiasParams& p, bool tan, int grid, hipStream_t stream) {
+hipError_t launch_pb(const PairBiasParams& p, bool tan, int64_t blocks, int cus, hipStream_t stream) {
+  const int64_t slots = static_cast<int64_t>(cus) * pb_occupancy<C, HB>();
+  const int grid = static_cast<int>(blocks < slots ? blocks : slots);
   if (tan)
     hipLaunchKernelGGL((pair_bias_kernel<C, HB, true>), dim3(grid), dim3(256), 0, stream, p);
   else
@@ -373,11 +382,11 @@ hipError_t launch_pb(const PairBiasParams& p, bool tan, int grid, hipStream_t st
 }
 
 template <int C>
-hipError_t launch_pb_c(const PairBiasParams& p, int H, bool tan, int grid, hipStream_t stream) {
+hipError_t launch_pb_c(const PairBiasParams& p, int H, bool tan, int64_t blocks, int cus, hipStream_t stream) {
   switch (H) {
-    case 16: return launch_pb<C, 1>(p, tan, grid, stream);
-    case 32: return launch_pb<C, 2>(p, tan, grid, stream);
-    case 64: return launch_pb<C, 4>(p, tan, grid, stream);
+    case 16: return launch_pb<C, 1>(p, tan, blocks, cus, stream);
+    case 32: return launch_pb<C, 2>(p, tan, blocks, cus, stream);
+    case 64: return launch_pb<C, 4>(p, tan, blocks, cus, stream);
     default: return hipErrorInvalidValue;
   }
 }
@@ -399,12 +408,11 @@ hipError_t launch_pair_bias(PairBiasParams p, int C, int H, bool tan, hipStream_
   p.parts = static_cast<int>(parts);
   p.n_items = p.B * parts;
   const int64_t blocks = (p.n_items + kPBWaves - 1) / kPBWaves;
-  const int grid = static_cast<int>(blocks < cus * 2 ? blocks : cus * 2);
   switch (C) {
-    case 32: return launch_pb_c<32>(p, H, tan, grid, stream);
-    case 64: return launch_pb_c<64>(p, H, tan, grid, stream);
-    case 96: return launch_pb_c<96>(p, H, tan, grid, stream);
-    case 128: return launch_pb_c<128>(p, H, tan, grid, stream);
+    case 32: return launch_pb_c<32>(p, H, tan, blocks, cus, stream);
+    case 64: return launch_pb_c<64>(p, H, tan, blocks, cus, stream);
+    case 96: return launch_pb_c<96>(p, H, tan, blocks, cus, stream);
+    case 128: return launch_pb_c<128>(p, H, tan, blocks, cus, stream);
     default: return hipErrorInvalidValue;
   }
 }
