@@ -127,11 +127,28 @@ CONFIGS = {
 }
 
 
+# Untimed run of the step before its warmup steps, in milliseconds of wall time. MI355X
+# boosts its clock for the first milliseconds of a heavy load and then throttles below the
+# level it settles at (c2: ~103 us per step over the first 2 ms, ~108 us over the next 5 ms,
+# ~100 us once settled), so K steps timed straight after a short warmup measure that
+# transient instead of the sustained rate a long walker run sees. Set by --settle-ms.
+SETTLE_MS = 100.0
+
+
 def timed(step, steps, warmup, stream):
     """Average milliseconds of ``step`` over ``steps`` steps after ``warmup``, with HIP
-    events recorded on the launch stream, bracketed by device synchronisation."""
+    events recorded on the launch stream, bracketed by device synchronisation. Before the
+    warmup steps the step runs untimed for ``SETTLE_MS`` of wall time."""
+    import time
+
     import torch
 
+    torch.cuda.synchronize()
+    t_end = time.perf_counter() + SETTLE_MS / 1e3
+    while time.perf_counter() < t_end:
+        for _ in range(8):
+            step(0)
+        torch.cuda.synchronize()
     for i in range(warmup):
         step(i)
     torch.cuda.synchronize()
@@ -378,7 +395,7 @@ def run_attention(args, cfg):
         "unit": "walkers/s",
         "n_gpus": 1,
         "steps": args.steps,
-        "warmup": args.warmup,
+        "warmup": args.warmup, "settle_ms": args.settle_ms,
         "ms_per_step": ms,
         "higher_is_better": True,
         "scaling": "weak",
@@ -483,7 +500,7 @@ def run_rect(args, cfg):
                "check": {"max_rel_err_vs_gpu": {"out": err}, "tol": 1e-5, "ok": err <= 1e-5}}
     line = {
         "metric": cfg.metric, "value": B * N / t_s, "unit": "queries/s", "n_gpus": 1, "steps": args.steps,
-        "warmup": args.warmup, "ms_per_step": ms, "higher_is_better": True, "scaling": "weak",
+        "warmup": args.warmup, "settle_ms": args.settle_ms, "ms_per_step": ms, "higher_is_better": True, "scaling": "weak",
         "vs_baseline": None, "dtype": "f32",
         "data": "synthetic (numpy default_rng, N(0,1) q/k/v, N(0,1)/sqrt(D) bias)",
         "config": {"workload": f"rect: {cfg.desc}", "B": B, "Nq": N, "Nk": N, "H": H, "D": D, "n_phys": n_phys},
@@ -567,7 +584,7 @@ def run_executor(args, cfg):
                "check": {"max_rel_err_vs_gpu": {"out": err}, "tol": 1e-5, "ok": err <= 1e-5}}
     line = {
         "metric": cfg.metric, "value": B / t_s, "unit": "walkers/s", "n_gpus": 1, "steps": args.steps,
-        "warmup": args.warmup, "ms_per_step": ms, "higher_is_better": True, "scaling": "weak",
+        "warmup": args.warmup, "settle_ms": args.settle_ms, "ms_per_step": ms, "higher_is_better": True, "scaling": "weak",
         "vs_baseline": None, "dtype": "f32", "data": "synthetic (numpy default_rng; T ~ N(0,1)/d_r, unit carriers)",
         "config": {"workload": f"{args.config}: {cfg.desc}", "walkers": B, "node_pairs": W, "groups": G, "d_r": R,
                    "merge_rank": Rm},
@@ -683,7 +700,7 @@ def run_trunk(args, cfg):
                "check": {"max_rel_err_vs_gpu": errs, "tol": tol, "ok": all(v <= tol for v in errs.values())}}
     line = {
         "metric": cfg.metric, "value": B / (ms / 1e3), "unit": "walkers/s", "n_gpus": 1, "steps": args.steps,
-        "warmup": args.warmup, "ms_per_step": ms, "higher_is_better": True, "scaling": "weak",
+        "warmup": args.warmup, "settle_ms": args.settle_ms, "ms_per_step": ms, "higher_is_better": True, "scaling": "weak",
         "vs_baseline": None, "dtype": "f32",
         "data": "synthetic (torch.randn on the GPU, seeded; weights N(0, fan_in^-1/2), small random biases)",
         "config": {"workload": f"{args.config}: {cfg.desc}", "B": B, "N": N, "H": H, "D": D, "n_phys": n_phys,
@@ -766,7 +783,7 @@ def run_wavefn(args, cfg):
                          "ok": d_la <= tol * max(1.0, float(np.max(np.abs(got_la)))) and d_ph <= tol}}
     line = {
         "metric": cfg.metric, "value": B / (ms / 1e3), "unit": "walkers/s", "n_gpus": 1, "steps": args.steps,
-        "warmup": args.warmup, "ms_per_step": ms, "higher_is_better": True, "scaling": "weak",
+        "warmup": args.warmup, "settle_ms": args.settle_ms, "ms_per_step": ms, "higher_is_better": True, "scaling": "weak",
         "vs_baseline": None, "dtype": "f32",
         "data": "synthetic (torch.randn on the GPU, seeded; weights N(0, fan_in^-1/2); every node merges)",
         "config": {"workload": f"{args.config}: {cfg.desc}", "walkers": B, "n_sites": n, "d_q": d_q, "d_z": d_z,
@@ -778,6 +795,7 @@ def run_wavefn(args, cfg):
 
 
 def main(argv=None):
+    global SETTLE_MS
     ap = argparse.ArgumentParser(description=__doc__.splitlines()[0])
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
@@ -785,12 +803,15 @@ def main(argv=None):
     ap.add_argument("--config", default="c2", choices=sorted(CONFIGS))
     ap.add_argument("--cpu-budget", type=float, default=15.0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--settle-ms", type=float, default=SETTLE_MS,
+                    help="untimed run of the step before the warmup steps (wall-time ms)")
     ap.add_argument("--generic", action="store_true",
                     help="force the LDS-streaming kernels (HZ_FLAG_GENERIC) for comparison")
     ap.add_argument("--copy-probe", type=int, default=0, metavar="MIB",
                     help="instead of a configuration, time device-to-device copies of MIB MiB "
                          "(the calibration kernel for rocprofv3 FETCH_SIZE / WRITE_SIZE)")
     args = ap.parse_args(argv)
+    SETTLE_MS = args.settle_ms
 
     if args.gpus != 1:
         print(f"bench.py measures one GPU only: this build runs the path on a single GPU (walkers shard "
