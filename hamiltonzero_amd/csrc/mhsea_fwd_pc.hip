@@ -101,10 +101,20 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, in
                                            static_cast<int>(bytes), 0x00020000);
 }
 
+// Output rows are written once and not read again by this kernel: non-temporal stores (the
+// nt cache-policy bit; same bytes). On MI355X at [1024, 64, 8, 32]: 0-1.3% faster without a
+// bias, 4% faster with one (the bias rows then keep more of the caches).
 __device__ __forceinline__ void buf_store4(__amdgpu_buffer_rsrc_t r, int voff, float a, float b,
                                            float c, float d) {
+  constexpr int kNonTemporal = 2;
   const u32x4_t v = {__float_as_uint(a), __float_as_uint(b), __float_as_uint(c), __float_as_uint(d)};
-  __builtin_amdgcn_raw_buffer_store_b128(v, r, voff, 0, 0);
+  __builtin_amdgcn_raw_buffer_store_b128(v, r, voff, 0, kNonTemporal);
+}
+
+// The producer's zero rows keep the default cache policy: non-temporal stores there made the
+// c2 shape 1.5% slower on MI355X.
+__device__ __forceinline__ void zero_row4(void* base, int64_t off) {
+  *reinterpret_cast<float4*>(static_cast<float*>(base) + off) = make_float4(0.f, 0.f, 0.f, 0.f);
 }
 
 __device__ __forceinline__ float buf_load1(__amdgpu_buffer_rsrc_t r, int voff) {
@@ -280,15 +290,15 @@ __device__ __forceinline__ void pc_producer(const FwdParams& p, char* lds, const
         if constexpr (GATED) {  // row of y for the pair (b, h - H/2)
           const int hh = H / 2;
           const int64_t off = ((static_cast<int64_t>(b) * N + site[u]) * hh + h % hh) * D + (it % Sh::C4) * 4;
-          store4<F32>(p.out, off, 0.f, 0.f, 0.f, 0.f);
+          zero_row4(p.out, off);
 #pragma unroll
-          for (int t = 0; t < T; ++t) store4<F32>(p.tout, t * p.y_tstride + off, 0.f, 0.f, 0.f, 0.f);
+          for (int t = 0; t < T; ++t) zero_row4(p.tout, t * p.y_tstride + off);
           continue;
         }
         const int64_t off = bnhd(b, site[u], h, N, H, D) + (it % Sh::C4) * 4;
-        if constexpr (!GIVEN_LSE) store4<F32>(p.out, off, 0.f, 0.f, 0.f, 0.f);
+        if constexpr (!GIVEN_LSE) zero_row4(p.out, off);
 #pragma unroll
-        for (int t = 0; t < T; ++t) store4<F32>(p.tout, t * p.t_stride + off, 0.f, 0.f, 0.f, 0.f);
+        for (int t = 0; t < T; ++t) zero_row4(p.tout, t * p.t_stride + off);
         if (!GIVEN_LSE && it % Sh::C4 == 0 && p.lse != nullptr)
           p.lse[(static_cast<int64_t>(b) * N + site[u]) * H + h] = p.masked_lse;
       }
