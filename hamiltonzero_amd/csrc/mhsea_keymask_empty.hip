@@ -15,10 +15,11 @@
 // and the tangent / cotangent formulas of the main kernels with this P. The derivative of
 // the penalty is 1 under autodiff, so dS keeps its usual form.
 //
-// One thread per (query or key) row; every thread of a workgroup serves the same walker and
-// row block and loops over the heads. A workgroup whose walker has a physical site exits at
-// once (one pass over the walker's mask bytes), so a call without empty walkers costs one
-// small launch. Plain fp32 loops: this serves a degenerate input, not a throughput path.
+// One thread per (query or key) row; a 64-thread workgroup serves one walker's block of 64
+// rows and loops over the heads (over the head pairs in the gated collapse), so a launch is
+// B * ceil(N / 64) workgroups whatever H is. A workgroup whose walker has a physical site
+// exits at once (one pass over the walker's mask bytes), so a call without empty walkers
+// costs one small launch. Plain fp32 loops: this serves a degenerate input, not a throughput path.
 #include "mhsea_device.h"
 #include "mhsea_launch.h"
 
@@ -285,7 +286,8 @@ hipError_t fwd_for(const FwdParams& p, int D, int T, bool given_lse, hipStream_t
     case 8: keymask_empty_fwd_kernel<S, 8><<<grid, kRows, 0, stream>>>(p, T, given_lse); break;
     case 16: keymask_empty_fwd_kernel<S, 16><<<grid, kRows, 0, stream>>>(p, T, given_lse); break;
     case 32: keymask_empty_fwd_kernel<S, 32><<<grid, kRows, 0, stream>>>(p, T, given_lse); break;
-    default: keymask_empty_fwd_kernel<S, 64><<<grid, kRows, 0, stream>>>(p, T, given_lse); break;
+    case 64: keymask_empty_fwd_kernel<S, 64><<<grid, kRows, 0, stream>>>(p, T, given_lse); break;
+    default: return hipErrorInvalidValue;
   }
   return hipGetLastError();
 }
@@ -297,7 +299,8 @@ hipError_t bwd_for(const BwdParams& p, int D, hipStream_t stream) {
     case 8: keymask_empty_bwd_kernel<S, 8><<<grid, kRows, 0, stream>>>(p); break;
     case 16: keymask_empty_bwd_kernel<S, 16><<<grid, kRows, 0, stream>>>(p); break;
     case 32: keymask_empty_bwd_kernel<S, 32><<<grid, kRows, 0, stream>>>(p); break;
-    default: keymask_empty_bwd_kernel<S, 64><<<grid, kRows, 0, stream>>>(p); break;
+    case 64: keymask_empty_bwd_kernel<S, 64><<<grid, kRows, 0, stream>>>(p); break;
+    default: return hipErrorInvalidValue;
   }
   return hipGetLastError();
 }
@@ -311,7 +314,9 @@ hipError_t launch_keymask_empty_fwd(const FwdParams& p, int D, int T, bool given
     switch (D) {
       case 8: keymask_empty_gated_kernel<8><<<grid, kRows, 0, stream>>>(p, T); break;
       case 16: keymask_empty_gated_kernel<16><<<grid, kRows, 0, stream>>>(p, T); break;
-      default: keymask_empty_gated_kernel<32><<<grid, kRows, 0, stream>>>(p, T); break;
+      case 32: keymask_empty_gated_kernel<32><<<grid, kRows, 0, stream>>>(p, T); break;
+      case 64: keymask_empty_gated_kernel<64><<<grid, kRows, 0, stream>>>(p, T); break;
+      default: return hipErrorInvalidValue;
     }
     return hipGetLastError();
   }

@@ -2,7 +2,7 @@
 
 The fused kernel's y = sigmoid(gate) * value and its tangents are compared with
 ``oracle.mhsea_oracle.gated_fwd_jvp`` (pinned in tests/test_gated_oracle.py) on seeded
-inputs, over T in {0, 1, 2}, D in {8, 16, 32}, prefix / scattered / empty masks, the key-mask
+inputs, over T in {0, 1, 2}, D in {8, 16, 32, 64}, prefix / scattered / empty masks, the key-mask
 mode, bias in both layouts, the kernel's own two-direction variant (D <= 16) and the two-pass
 route (D = 32), and grids where one workgroup walks several head pairs; and
 against the unfused composition (hz_mhsea_fwd_jvp, then the collapse in torch) at c2's shape.
@@ -277,4 +277,59 @@ def test_gated_bwd_matches_oracle(case):
     for name, got, ref in zip(("dq", "dk", "de", "dv"), (dq, dk, de, dv), want):
         if got is None:
             continue
+        assert rel(got.cpu().numpy(), ref) <= TOL, name
+
+
+@pytest.mark.parametrize("T,N,with_e", [(0, 64, False), (2, 64, True), (1, 130, True), (2, 96, False)])
+def test_gated_key_mask_empty_walkers_d64(T, N, with_e):
+    """Key-mask mode at D = 64 with walkers that have no physical site (forced, not drawn):
+    the fix-up kernel for those walkers is instantiated per head dimension, so it must write
+    exactly their rows at D = 64 and leave every other walker's y and ydot as the main kernel
+    wrote them. Both checked against the float64 oracle, per walker group."""
+    from hamiltonzero_amd import kernels
+
+    B, H, D = 7, 4, 64
+    _say(f"gated key-mask empty walkers D=64 T={T} N={N} e={with_e}")
+    q, k, v, e, mask, tq, tk, tv, te = make(60 + T + N, B, N, H, D, T, "scattered", with_e, "qhk")
+    empty = np.array([1, 4, 6])
+    mask[empty] = False
+    full = np.setdiff1d(np.arange(B), empty)
+    dev = lambda x: None if x is None else torch.from_numpy(np.ascontiguousarray(x)).cuda()  # noqa: E731
+    kw = dict(scale=D ** -0.5, key_mask=True, e_layout="qhk")
+    if T == 0:
+        y, ty = kernels.mhsea_fwd_jvp_gated(dev(q), dev(k), dev(v), dev(mask), e=dev(e), **kw)
+    else:
+        y, ty = kernels.mhsea_fwd_jvp_gated(dev(q), dev(k), dev(v), dev(mask), dev(tq[:T]), dev(tk[:T]), dev(tv[:T]),
+                                            e=dev(e), et=None if te is None else dev(te[:T]), **kw)
+    torch.cuda.synchronize()
+    y = y.cpu().numpy()
+    for t in range(max(T, 1)):
+        ey, eyd = O.gated_fwd_jvp(q, k, e, v, mask, tq[t], tk[t], None if te is None else te[t], tv[t], **kw)
+        if t == 0:
+            assert rel(y[full], ey[full]) <= TOL, "y of walkers with a physical site"
+            assert rel(y[empty], ey[empty]) <= TOL, "y of walkers with no physical site"
+        if T:
+            got = ty[t].cpu().numpy()
+            assert rel(got[full], eyd[full]) <= TOL, f"ydot {t}, walkers with a physical site"
+            assert rel(got[empty], eyd[empty]) <= TOL, f"ydot {t}, walkers with no physical site"
+
+
+def test_gated_bwd_key_mask_empty_walkers_d64():
+    """The gated reverse mode at D = 64 in key-mask mode with forced empty walkers, against
+    the oracle's gated_vjp (dq, dk, de, dv over the whole batch)."""
+    from hamiltonzero_amd import kernels
+
+    B, N, H, D = 5, 64, 4, 64
+    _say("gated bwd key-mask empty walkers D=64")
+    q, k, v, e, mask, *_ = make(71, B, N, H, D, 0, "scattered", True, "qhk")
+    mask[[0, 3]] = False
+    dy = np.random.default_rng(72).standard_normal((B, N, H // 2, D), dtype=np.float32)
+    dev = lambda x: None if x is None else torch.from_numpy(np.ascontiguousarray(x)).cuda()  # noqa: E731
+    kw = dict(scale=D ** -0.5, key_mask=True, e_layout="qhk")
+    out, lse = kernels.mhsea_fwd(dev(q), dev(k), dev(v), dev(mask), dev(e), **kw)
+    dq, dk, de, dv = kernels.mhsea_bwd_gated(dev(q), dev(k), dev(v), dev(mask), lse, out, dev(dy), dev(e),
+                                             want_de=True, **kw)
+    torch.cuda.synchronize()
+    want = O.gated_vjp(q, k, e, v, mask, dy, **kw)
+    for name, got, ref in zip(("dq", "dk", "de", "dv"), (dq, dk, de, dv), want):
         assert rel(got.cpu().numpy(), ref) <= TOL, name
