@@ -524,8 +524,8 @@ int hz_compiled_wavefunction(hipStream_t stream, const float* q, const float* q_
   HZ_REQUIRE(leaf_V);
   HZ_REQUIRE(leaf_U);
   HZ_REQUIRE(leaf_h);
-  HZ_REQUIRE(merge_T);
-  if (n_sites > 1) {
+  if (n_sites > 1) {  // one site: no merge level, so no merge operand is read
+    HZ_REQUIRE(merge_T);
     HZ_REQUIRE(merge_V);
     HZ_REQUIRE(merge_U);
     HZ_REQUIRE(merge_h);

@@ -79,6 +79,8 @@ int64_t hz_compiled_wavefunction_workspace(int64_t B, int64_t n_sites, int64_t d
  *   packed per-level storage (model.py:58-90: level l uses its first n_sites >> (l + 1) rows;
  *   L = log2 n_sites), readout_V [d_m, R_out], readout_U [R_out, 2], readout_h [R_out];
  *   outputs log_abs [B], phase [B]; workspace of hz_compiled_wavefunction_workspace() bytes.
+ *   With n_sites == 1 there is no merge level: merge_T, merge_V, merge_U, merge_h and
+ *   opcodes are not read and may be NULL.
  * n_sites a power of two (level_widths, compiled/types.py:166-169), d_r = 32, d_m = G d_r <=
  * 2048. Fine-tune sizes: d_q 4, d_z 32, R_leaf 1536, G 48, R_merge 1024, R_out 64
  * (config.py:21-29,189-190; tree.py:2360-2361).

@@ -229,6 +229,7 @@ def test_compiled_wavefunction_rejects_bad_arguments(lib):
         (dict(merge_eps=float("nan")), _native.HZ_EINVAL, "merge_eps"),
         (dict(q=None), _native.HZ_ENULL, "q must not be NULL"),
         (dict(opcodes=None), _native.HZ_ENULL, "opcodes"),
+        (dict(merge_T=None), _native.HZ_ENULL, "merge_T"),
         (dict(leaf_h=A + 4), _native.HZ_EALIGN, "leaf_h"),
     ]
     for over, code, needle in cases:
