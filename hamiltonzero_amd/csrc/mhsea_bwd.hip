@@ -181,7 +181,7 @@ __global__ void __launch_bounds__(256) mhsea_bwd_q_kernel(const BwdParams p) {
           n = key_all ? j : idx[j];
           if constexpr (HAS_E) sv += load1<S>(p.e, e_row + static_cast<int64_t>(n) * p.e_sk);
         }
-        const float pv = valid ? exp2f(sv * kLog2e - lse2) : 0.f;
+        const float pv = valid ? clamp01(exp2f(sv * kLog2e - lse2)) : 0.f;
         dsv[r] = pv * (dp[r] - delta);
         if (valid && p.de != nullptr) store1<S>(p.de, e_row + static_cast<int64_t>(n) * p.e_sk, dsv[r]);
       }
@@ -323,7 +323,7 @@ __global__ void __launch_bounds__(256) mhsea_bwd_kv_kernel(const BwdParams p) {
                                     static_cast<int64_t>(ksite) * p.e_sk);
           }
         }
-        pv[r] = valid ? exp2f(sv * kLog2e - L2s[il]) : 0.f;
+        pv[r] = valid ? clamp01(exp2f(sv * kLog2e - L2s[il])) : 0.f;
         dsv[r] = pv[r] * (dp[r] - Dls[il]);
       }
       // dv^T[d][key] += dout^T[d][query] P[query][key];  dk^T += (scale q)^T dS

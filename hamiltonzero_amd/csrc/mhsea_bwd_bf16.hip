@@ -293,7 +293,7 @@ __global__ void __launch_bounds__(256, 2) mhsea_bwd_bf16_kernel(const BwdParams 
               ks = __shfl(kperm, j & 63, 64);
               if (valid) sv += load1<BF16>(p.e, e_row + static_cast<int64_t>(ks) * p.e_sk);
             }
-            pv[r] = valid ? fast_exp2(sv * kLog2e - lse2) : 0.f;
+            pv[r] = valid ? lse_weight(sv * kLog2e - lse2) : 0.f;
             dsv[jt][r] = pv[r] * (dp[r] - delta);
             if (p.de != nullptr) {
               if constexpr (!HAS_E) ks = __shfl(kperm, j & 63, 64);

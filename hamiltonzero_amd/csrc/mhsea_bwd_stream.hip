@@ -215,7 +215,7 @@ __global__ void __launch_bounds__(256, (BwdStreamShape<D>::kWavesPerEu))
               ks = __shfl(kperm, j & 63, 64);
               if (valid) sv += load1<S>(p.e, e_row + static_cast<int64_t>(ks) * p.e_sk);
             }
-            const float pv = valid ? fast_exp2(sv * kLog2e - lse2) : 0.f;
+            const float pv = valid ? lse_weight(sv * kLog2e - lse2) : 0.f;
             dsv[r] = pv * (dp[r] - delta);
             if (p.de != nullptr) {
               if constexpr (!HAS_E) ks = __shfl(kperm, j & 63, 64);
@@ -286,7 +286,7 @@ __global__ void __launch_bounds__(256, (BwdStreamShape<D>::kWavesPerEu))
                 sv += load1<S>(p.e, e_walker + static_cast<int64_t>(qs2) * p.e_sq +
                                         static_cast<int64_t>(ksite) * p.e_sk);
             }
-            pv[r] = valid ? fast_exp2(sv * kLog2e - L2s[il]) : 0.f;
+            pv[r] = valid ? lse_weight(sv * kLog2e - L2s[il]) : 0.f;
             dsv[r] = pv[r] * (dp[r] - Dls[il]);
           }
 #pragma unroll

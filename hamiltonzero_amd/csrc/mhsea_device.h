@@ -33,6 +33,18 @@ __device__ __forceinline__ v4f zero4() { return v4f{0.f, 0.f, 0.f, 0.f}; }
 // the row maximum.
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
+// A softmax weight rebuilt from a stored lse, P = 2^(s log2e - lse log2e), clamped to [0, 1]
+// (one med3, or the clamp bit of v_exp_f32). P <= 1 by construction, but the two products
+// are rounded separately: in a row whose every score is the same huge number (a bias of -1e30
+// on every key, as the route decoder passes for queries with no valid key,
+// route_pointer.py:2042-2048) lse equals that score up to rounding and the difference is
+// +-1 ulp of 1.4e30, whose 2^x overflows. The reference's exp(s - lse) is exactly 1 there
+// (custom_gradients.py, mhsea_tuned_jvp.py: both in natural units); clamped, such a row
+// gets weight 1 or 0 and stays finite. Elsewhere the clamp changes at most a rounding
+// excess above 1.
+__device__ __forceinline__ float clamp01(float x) { return __builtin_amdgcn_fmed3f(x, 0.f, 1.f); }
+__device__ __forceinline__ float lse_weight(float x) { return clamp01(fast_exp2(x)); }
+
 // bfloat16 <-> float32. Round-to-nearest-even on the way down; NaN stays NaN.
 __device__ __forceinline__ float bf16_to_f32(uint16_t x) {
   return __uint_as_float(static_cast<uint32_t>(x) << 16);

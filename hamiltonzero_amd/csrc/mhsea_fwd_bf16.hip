@@ -327,7 +327,7 @@ __global__ void __launch_bounds__(256, ((D == 64 && T > 0) ? 2 : 3)) mhsea_fwd_b
 #pragma unroll
       for (int jt = 0; jt < NJT; ++jt)
 #pragma unroll
-        for (int r = 0; r < 4; ++r) sc[jt][r] = fast_exp2(sc[jt][r] - lse2);
+        for (int r = 0; r < 4; ++r) sc[jt][r] = lse_weight(sc[jt][r] - lse2);
     } else {
       const float mnew = fmaxf(m2, group_max(mx));
       if (MULTI && kc > 0) {

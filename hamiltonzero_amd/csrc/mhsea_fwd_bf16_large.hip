@@ -408,7 +408,7 @@ __global__ void __launch_bounds__(kThreads, 1) mhsea_fwd_bf16_large_kernel(const
 #pragma unroll
       for (int jt = 0; jt < NJT; ++jt)
 #pragma unroll
-        for (int r = 0; r < 4; ++r) sc[jt][r] = fast_exp2(fmaf(sc[jt][r], smul, -lse2));
+        for (int r = 0; r < 4; ++r) sc[jt][r] = lse_weight(fmaf(sc[jt][r], smul, -lse2));
     } else {
       mx = group_max(mx);
       const bool need = mx > m2 + kRescale;  // also true for the first chunk (m2 = -inf)

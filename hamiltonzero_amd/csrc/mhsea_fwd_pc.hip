@@ -702,7 +702,7 @@ __device__ __forceinline__ void pc_tile(const FwdParams& p, const char* buf, con
 #pragma unroll
     for (int jt = 0; jt < NJ; ++jt)
 #pragma unroll
-      for (int r = 0; r < 4; ++r) sc[jt][r] = fast_exp2(sc[jt][r] - lse2);
+      for (int r = 0; r < 4; ++r) sc[jt][r] = lse_weight(sc[jt][r] - lse2);
   } else {
     mx = group_max(mx);
 #pragma unroll

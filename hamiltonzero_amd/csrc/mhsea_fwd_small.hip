@@ -223,7 +223,7 @@ __global__ void __launch_bounds__(256, 2) mhsea_fwd_small_kernel(const FwdParams
 #pragma unroll
       for (int kt = 0; kt < NKT; ++kt)
 #pragma unroll
-        for (int r = 0; r < 4; ++r) st[kt][r] = exp2f(st[kt][r] - lse2);
+        for (int r = 0; r < 4; ++r) st[kt][r] = clamp01(exp2f(st[kt][r] - lse2));
     } else {
       mx = group_max(mx);
 #pragma unroll

@@ -308,7 +308,7 @@ __global__ void __launch_bounds__(256, (StreamShape<D, T>::kWavesPerEu))
 #pragma unroll
         for (int jt = 0; jt < NJT; ++jt)
 #pragma unroll
-          for (int r = 0; r < 4; ++r) sc[jt][r] = fast_exp2(sc[jt][r] - lse2);
+          for (int r = 0; r < 4; ++r) sc[jt][r] = lse_weight(sc[jt][r] - lse2);
       } else {
         mx = group_max(mx);
 #pragma unroll
