@@ -43,6 +43,9 @@ WAVEFN_METRIC = ("compiled per-walker wavefunction (leaf, 6 merge levels, readou
                  "B=1024, 64 sites, fine-tune ranks; % of MFMA roofline")
 TRUNK_METRIC = ("trunk attention block after W_QKV (ln_edge + bias_mlp producer, fwd+JVP with the gate collapse, "
                 "W_O), walkers/sec at B=1024,L=64; % of MFMA roofline")
+VJP_METRIC = "fwd+VJP attention walkers/sec at B=1024,L=64 (fp32 training path); % of MFMA/HBM roofline"
+GATE_VJP_METRIC = ("fwd+VJP attention with the sigmoid-gate head collapse and the bias cotangent, walkers/sec at "
+                   "B=1024,L=64; % of MFMA/HBM roofline")
 HBM_PEAK_GBS = 8000.0
 FP32_PEAK_TFLOPS = 157.3
 BF16_PEAK_TFLOPS = 2516.6
@@ -119,6 +122,25 @@ CONFIGS = {
                     "the trunk's attention block after W_QKV: edge [1024,64,64,96] and its tangent -> "
                     "ln_edge + bias_mlp -> e, e_t [1024,64,32,64] -> gated fwd+JVP [1024,64,32,16] -> y, ydot "
                     "[1024,64,256] -> W_O [256,512] -> delta, delta_t [1024,64,512], 36/64 physical sites", cpu_sample=4, metric=TRUNK_METRIC),
+    # The reference's production gradient path in float32 (jax.value_and_grad through the
+    # primitive's transpose rule, optim/production.py:238 -> mhsea_tuned.py:206-221 ->
+    # custom_gradients.py:78-347) at c2's shape: forward (out, lse), then the VJP.
+    "c2vjp": Config("fwd_vjp", 1024, 64, 8, 32, 36, 0, "f32", 1,
+                    "forward + VJP (training), fp32, [1024,64,8,32], 36/64 physical sites: forward (out, lse), "
+                    "then dq, dk, dv", metric=VJP_METRIC),
+    # The same training path at c3's shape in float32, the precision the reference trains in
+    # (pallas_attention.py:16-19 admits float32 only).
+    "c3f32": Config("fwd_vjp", 4096, 64, 8, 64, 48, 0, "f32", 2,
+                    "forward + VJP (training), fp32, [4096,64,8,64], 48/64 physical sites: forward (out, lse), "
+                    "then dq, dk, dv", cpu_sample=16, metric=VJP_METRIC.replace("B=1024", "B=4096")),
+    # The trunk's reverse mode: forward (out, lse) of its attention call, then the gate
+    # collapse's cotangent and the attention backward with the bias cotangent de
+    # (hz_mhsea_bwd_gated), at [1024,64,32,16] with pair bias.
+    "gate_trunk_vjp": Config("fwd_vjp_gated", 1024, 64, 32, 16, 36, 0, "f32", 1,
+                             "the trunk's attention call in reverse mode: forward (out, lse) of [1024,64,32,16] "
+                             "with pair bias e [1024,64,32,64], then dy [1024,64,16,16] -> collapse cotangent -> "
+                             "dq, dk, dv, de, 36/64 physical sites", with_e=True, cpu_sample=16,
+                             metric=GATE_VJP_METRIC),
     # The large-N evaluation forward (noncausal_bias_mha via pallas_rectangular_edge_attention):
     # one system, all queries against all keys, dense [Nq, Nk, H] bias.
     "rect": Config("rect", 1, 4096, 16, 64, 4000, 0, "f32", 5,
@@ -186,10 +208,15 @@ def algorithmic(work, B, N, H, D, n_phys, T, esize, with_e=False):
     elif work == "fwd_vjp":
         # fwd: q,k,v in, out + lse out; bwd: q,k,v,out,dout + lse in, dq,dk,dv out
         n_in, n_out, g_mult, lse_b, n_e = 3 + 5, 1 + 3, 6, 2 * N * H * 4, 2
+    elif work == "fwd_vjp_gated":
+        # fwd: q,k,v,e in, out + lse out; bwd: q,k,v,e,out + lse and dy (half a tensor) in,
+        # dq,dk,dv and de out (de written on every pair, zeros included)
+        n_in, n_out, g_mult, lse_b, n_e = 3 + 4.5, 1 + 3, 6, 2 * N * H * 4, 2
     else:
         raise ValueError(work)
-    e_pad = n_e * N * H * N * esize if with_e else 0
-    e_eff = n_e * n_phys * H * n_phys * esize if with_e else 0
+    n_e_out = 1 if work == "fwd_vjp_gated" else 0
+    e_pad = (n_e + n_e_out) * N * H * N * esize if with_e else 0
+    e_eff = (n_e * n_phys * n_phys + n_e_out * N * N) * H * esize if with_e else 0
     padded_bytes = int(B * (N * rowb * (n_in + n_out) + N + lse_b + e_pad))
     eff_bytes = int(B * (n_phys * rowb * n_in + N * rowb * n_out + N + lse_b + e_eff))
     padded_flops = B * H * g_mult * 2 * N * N * D
@@ -229,6 +256,17 @@ def traffic_from_profile(config):
     with open(path) as fh:
         rec = json.load(fh)
     return rec.get("traffic_bytes_per_launch")
+
+
+def issued_flops_from_profile(config):
+    """Matrix flops the kernels of one step issue (rocprofv3 --pmc SQ_INSTS_VALU_MFMA_MOPS_*
+    x 512, summed over the step's launches), if the committed profile summary records them.
+    Differs from the algorithmic flops where MFMA tiles carry padding rows."""
+    path = os.path.join(ROOT, "profiles", f"traffic_{config}.json")
+    if not os.path.exists(path):
+        return None
+    with open(path) as fh:
+        return json.load(fh).get("mfma_flops_issued_per_step")
 
 
 def copy_probe(mib, steps, warmup):
@@ -280,6 +318,8 @@ def draw_inputs(cfg):
             a[nm] = np.stack([t[i] for t in tans])
     if cfg.work == "fwd_vjp":
         a["dout"] = draw(shape, 1.0)
+    if cfg.work == "fwd_vjp_gated":
+        a["dy"] = draw((cfg.B, cfg.N, cfg.H // 2, cfg.D), 1.0)
     if cfg.with_e:
         a["e"] = draw(eshape, 0.5)
         if cfg.T:
@@ -304,10 +344,14 @@ def run_attention(args, cfg):
     shape = (B, N, H, D)
     host = draw_inputs(cfg)
 
-    # Configurations whose whole working set fits in the 256 MB Infinity Cache are timed on
-    # enough copies of their buffers, used in turn, that each step reads from HBM.
+    # Configurations whose touched bytes per step (the mask-aware figure: the kernels read
+    # physical rows only) are below twice the 256 MB Infinity Cache run on enough copies of
+    # their buffers, used in turn, that no step finds its inputs left in the cache by the
+    # previous steps. --buffer-sets overrides the count (1: every step on the same buffers).
     alg = algorithmic(cfg.work, B, N, H, D, cfg.n_phys, T, esize, cfg.with_e)
-    copies = 1 if alg["padded_bytes"] >= INFINITY_CACHE_BYTES else -(-2 * INFINITY_CACHE_BYTES // alg["padded_bytes"])
+    copies = max(1, -(-2 * INFINITY_CACHE_BYTES // alg["eff_bytes"]))
+    if args.buffer_sets:
+        copies = args.buffer_sets
 
     def dev_set():
         d = {}
@@ -324,9 +368,13 @@ def run_attention(args, cfg):
             del d["out"]
             d["y"] = torch.empty((B, N, H // 2, D), dtype=tdt, device=dev)
             d["ty"] = torch.empty((T, B, N, H // 2, D), dtype=tdt, device=dev)
-        if cfg.work == "fwd_vjp":
+        if cfg.work in ("fwd_vjp", "fwd_vjp_gated"):
             for nm in ("dq", "dk", "dv"):
                 d[nm] = torch.empty(shape, dtype=tdt, device=dev)
+        if cfg.work == "fwd_vjp_gated":
+            d["dout_work"] = torch.empty(shape, dtype=torch.float32, device=dev)
+            if cfg.with_e:
+                d["de"] = torch.empty((B, N, H, N), dtype=tdt, device=dev)
         return d
 
     sets = [dev_set() for _ in range(copies)]
@@ -361,6 +409,12 @@ def run_attention(args, cfg):
             _native.check(lib.hz_mhsea_fwd_jvp_gated(s, q, k, e, v, m, P(d, "qt", b0), P(d, "kt", b0), et,
                                                      P(d, "vt", b0), T, P(d, "y", b0, row // 2),
                                                      P(d, "ty", b0, row // 2), nb, N, H, D, 1.0, 0))
+        elif cfg.work == "fwd_vjp_gated":
+            lse = P(d, "lse", b0, N * H * 4)
+            _native.check(lib.hz_mhsea_fwd(s, q, k, e, v, m, P(d, "out", b0), lse, nb, N, H, D, hz_dtype, 1.0, fl))
+            _native.check(lib.hz_mhsea_bwd_gated(s, q, k, e, v, m, lse, P(d, "out", b0), P(d, "dy", b0, row // 2),
+                                                 P(d, "dq", b0), P(d, "dk", b0), P(d, "de", b0, erow),
+                                                 P(d, "dv", b0), P(d, "dout_work", b0), nb, N, H, D, 1.0, fl))
         else:
             lse = P(d, "lse", b0, N * H * 4)
             _native.check(lib.hz_mhsea_fwd(s, q, k, e, v, m, P(d, "out", b0), lse, nb, N, H, D, hz_dtype, 1.0, fl))
@@ -384,6 +438,12 @@ def run_attention(args, cfg):
     roof_mask["basis"] = "mask-aware algorithmic bytes/flops (physical rows and pairs in, all rows out)"
     roof_mask["bytes_per_step"] = alg["eff_bytes"]
     roof_mask["flops_per_step"] = alg["eff_flops"]
+    issued = issued_flops_from_profile(args.config)
+    if issued:
+        peak_c = BF16_PEAK_TFLOPS if cfg.dtype == "bf16" else FP32_PEAK_TFLOPS
+        roof["issued"] = {"basis": "matrix flops the kernels issue (rocprofv3 MFMA MOPS x 512, profiles/)",
+                          "flops_per_step": issued, "achieved": issued / t_s / 1e12, "unit": "TFLOP/s",
+                          "peak": peak_c, "frac": issued / t_s / 1e12 / peak_c}
 
     cpu = None
     if not args.no_cpu_baseline:
@@ -404,7 +464,7 @@ def run_attention(args, cfg):
         "data": "synthetic (numpy default_rng, N(0,1)/sqrt(D) q/k/v, N(0,1) tangents)",
         "config": {"workload": f"{args.config}: {cfg.desc}", "B": B, "N": N, "H": H, "D": D,
                    "n_phys": cfg.n_phys, "T": T, "work": cfg.work, "walkers_per_launch": cfg.chunk,
-                   "bias": cfg.with_e, "buffer_sets": copies,
+                   "bias": cfg.with_e, "buffer_sets": copies, "touched_bytes_per_set": alg["eff_bytes"],
                    "kernels": "generic" if args.generic else "auto"},
         "roofline": roof,
         "roofline_mask_aware": roof_mask,
@@ -807,6 +867,9 @@ def main(argv=None):
                     help="untimed run of the step before the warmup steps (wall-time ms)")
     ap.add_argument("--generic", action="store_true",
                     help="force the LDS-streaming kernels (HZ_FLAG_GENERIC) for comparison")
+    ap.add_argument("--buffer-sets", type=int, default=0, metavar="N",
+                    help="run the attention step over N copies of its buffers in turn (default: enough that the "
+                         "touched bytes of the copies exceed twice the 256 MB Infinity Cache)")
     ap.add_argument("--copy-probe", type=int, default=0, metavar="MIB",
                     help="instead of a configuration, time device-to-device copies of MIB MiB "
                          "(the calibration kernel for rocprofv3 FETCH_SIZE / WRITE_SIZE)")

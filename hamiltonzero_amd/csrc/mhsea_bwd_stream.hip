@@ -32,7 +32,11 @@ struct BwdStreamShape {
   static constexpr int kItems = KC * C4;
   static constexpr int kPerThread = (kItems + 255) / 256;
   static constexpr size_t kLdsBytes = static_cast<size_t>(4 * kTileFloats + 2 * KC) * 4;
-  static constexpr int kWavesPerEu = D == 64 ? 2 : 3;
+  // D = 64: one wave per SIMD, so the next item's prefetched rows (80 registers) and the
+  // phase-B accumulators fit without scratch (two waves spilled 180-220 bytes per lane and
+  // ran 2.4% slower at [4096, 64, 8, 64] fp32). D = 32 keeps three waves with 44-76 bytes of
+  // scratch: two waves without it ran 2.7% slower at [1024, 64, 8, 32].
+  static constexpr int kWavesPerEu = D == 64 ? 1 : 3;
 };
 
 struct Sites {

@@ -64,6 +64,16 @@ def fwd_vjp(q, k, v, mask, dout, e=None):
     return out, pullback(dout)
 
 
+def fwd_vjp_gated(q, k, v, mask, dy, e=None):
+    """(y, (dq, dk, dv[, de])) by reverse-mode autodiff of :func:`gated` (the bias is a
+    differentiated input when given)."""
+    if e is None:
+        y, pullback = torch.func.vjp(lambda a, b, c: gated(a, b, c, mask), q, k, v)
+    else:
+        y, pullback = torch.func.vjp(lambda a, b, c, d: gated(a, b, c, mask, d), q, k, v, e)
+    return y, pullback(dy)
+
+
 def host_cpu_model() -> str:
     try:
         with open("/proc/cpuinfo") as fh:
@@ -99,10 +109,11 @@ def default_threads() -> int:
 
 
 def time_walkers_per_s(work: str, inputs: dict, budget_s: float = 15.0, threads: int | None = None) -> dict:
-    """Time ``work`` ('fwd', 'fwd_jvp', 'fwd_jvp_gated' or 'fwd_vjp') on the walkers of
-    ``inputs`` (CPU float32 tensors: q, k, v, mask, optional e; tangents qt, kt, vt, et as
-    [T, ...] for the forward-mode works; dout for 'fwd_vjp'). Returns walkers/s and the
-    outputs of the last repetition ('out', 'tout' [T, ...], 'y', 'ty', 'dq', 'dk', 'dv')."""
+    """Time ``work`` ('fwd', 'fwd_jvp', 'fwd_jvp_gated', 'fwd_vjp' or 'fwd_vjp_gated') on the
+    walkers of ``inputs`` (CPU float32 tensors: q, k, v, mask, optional e; tangents qt, kt,
+    vt, et as [T, ...] for the forward-mode works; dout for 'fwd_vjp', dy for
+    'fwd_vjp_gated'). Returns walkers/s and the outputs of the last repetition ('out', 'tout'
+    [T, ...], 'y', 'ty', 'dq', 'dk', 'dv', 'de')."""
     threads = threads or default_threads()
     torch.set_num_threads(threads)
     q, k, v, mask, e = (inputs.get(n) for n in ("q", "k", "v", "mask", "e"))
@@ -125,6 +136,13 @@ def time_walkers_per_s(work: str, inputs: dict, budget_s: float = 15.0, threads:
         def fn():
             out, (dq, dk, dv) = fwd_vjp(q, k, v, mask, inputs["dout"], e)
             return {"out": out, "dq": dq, "dk": dk, "dv": dv}
+    elif work == "fwd_vjp_gated":
+        def fn():
+            _, grads = fwd_vjp_gated(q, k, v, mask, inputs["dy"], e)
+            res = dict(zip(("dq", "dk", "dv"), grads[:3]))
+            if e is not None:
+                res["de"] = grads[3]
+            return res
     else:
         raise ValueError(work)
     with torch.no_grad() if work == "fwd" else torch.enable_grad():

@@ -62,3 +62,33 @@ def test_merge_level_config_is_fine_tune_shaped():
     48 groups of d_r = 32 (merge_dim 1536), merge_rank 1024, 1024 walkers x 32 node pairs."""
     cfg = bench.CONFIGS["merge"]
     assert (cfg.work, cfg.B, cfg.N, cfg.H, cfg.D, cfg.n_phys) == ("executor", 1024, 32, 48, 32, 1024)
+
+
+def test_reverse_mode_configs():
+    """c2vjp: the fp32 training path at c2's shape, charged 12 tensor passes + 2 lse passes
+    and 6G; gate_trunk_vjp: the gated reverse mode at the trunk's shape, charged the
+    forward's q, k, v, e, the backward's q, k, v, e, out and dy (half a tensor), the outputs
+    out, dq, dk, dv and de (every pair), and 6G."""
+    c = bench.CONFIGS["c2vjp"]
+    a = bench.algorithmic(c.work, c.B, c.N, c.H, c.D, c.n_phys, c.T, 4, c.with_e)
+    row = c.H * c.D * 4
+    assert a["padded_bytes"] == c.B * (c.N * row * 12 + c.N + 2 * c.N * c.H * 4)
+    assert a["padded_flops"] == c.B * c.H * 6 * 2 * c.N * c.N * c.D
+    g = bench.CONFIGS["gate_trunk_vjp"]
+    a = bench.algorithmic(g.work, g.B, g.N, g.H, g.D, g.n_phys, g.T, 4, g.with_e)
+    row = g.H * g.D * 4
+    e_all = g.N * g.H * g.N * 4
+    assert a["padded_bytes"] == g.B * (g.N * row * 11.5 + g.N + 2 * g.N * g.H * 4 + 3 * e_all)
+    e_phys = g.n_phys * g.H * g.n_phys * 4
+    assert a["eff_bytes"] == int(g.B * (g.n_phys * row * 7.5 + g.N * row * 4 + g.N + 2 * g.N * g.H * 4
+                                         + 2 * e_phys + e_all))
+    assert a["padded_flops"] == g.B * g.H * 6 * 2 * g.N * g.N * g.D
+
+
+def test_buffer_rotation_covers_twice_the_infinity_cache():
+    """The default buffer-set count makes the touched (mask-aware) bytes of all sets exceed
+    twice the 256 MB Infinity Cache: c2's 361 MB per set needs two."""
+    c = bench.CONFIGS["c2"]
+    a = bench.algorithmic(c.work, c.B, c.N, c.H, c.D, c.n_phys, c.T, 4, c.with_e)
+    sets = max(1, -(-2 * bench.INFINITY_CACHE_BYTES // a["eff_bytes"]))
+    assert sets == 2 and sets * a["eff_bytes"] >= 2 * bench.INFINITY_CACHE_BYTES
