@@ -38,6 +38,8 @@ METRIC = "fwd+JVP attention walkers/sec at B=1024,L=64; % of MFMA/HBM roofline"
 GATE_METRIC = ("fwd+JVP attention with the sigmoid-gate head collapse fused, walkers/sec at B=1024,L=64; "
                "% of MFMA/HBM roofline")
 RECT_METRIC = "rectangular large-N forward (noncausal_bias_mha) query rows/sec; % of MFMA/HBM roofline"
+RECT_GATE_METRIC = ("large-N attention tail (rectangular attention + gate collapse fused, W_O) query rows/sec; "
+                    "% of MFMA roofline")
 EXECUTOR_METRIC = "compiled-executor merge level (quadrilinear merge + factorized apply) walkers/sec; % of MFMA roofline"
 WAVEFN_METRIC = ("compiled per-walker wavefunction (leaf, 6 merge levels, readout -> log|psi|, phase) walkers/sec at "
                  "B=1024, 64 sites, fine-tune ranks; % of MFMA roofline")
@@ -60,13 +62,14 @@ class Config:
     tangents) present. cpu_sample: walkers of the CPU baseline's sample."""
 
     def __init__(self, work, B, N, H, D, n_phys, T, dtype, seed, desc, *, chunk=None, with_e=False,
-                 cpu_sample=64, metric=METRIC):
+                 cpu_sample=64, metric=METRIC, d_c=0):
         self.work, self.B, self.N, self.H, self.D = work, B, N, H, D
         self.n_phys, self.T, self.dtype, self.seed, self.desc = n_phys, T, dtype, seed, desc
         self.chunk = chunk or B
         self.with_e = with_e
         self.cpu_sample = cpu_sample
         self.metric = metric
+        self.d_c = d_c
 
 
 CONFIGS = {
@@ -141,6 +144,13 @@ CONFIGS = {
                              "with pair bias e [1024,64,32,64], then dy [1024,64,16,16] -> collapse cotangent -> "
                              "dq, dk, dv, de, 36/64 physical sites", with_e=True, cpu_sample=16,
                              metric=GATE_VJP_METRIC),
+    # The large-N caller's attention tail (sequence_trunk.py:973-984): the rectangular
+    # attention with the head collapse fused, then W_O [n_heads * d_head, d_c] (d_c = 512,
+    # config.py:19) with the row mask.
+    "rect_gate": Config("rect_gate", 1, 4096, 16, 64, 4000, 0, "f32", 5,
+                        "large-N attention tail: rectangular attention with the gate collapse fused (one system, "
+                        "Nq=Nk=4096, H=16 -> 8 gated heads, D=64, dense bias, 4000/4096 physical sites) -> y "
+                        "[4096,8,64] -> W_O [512,512] on the physical rows", metric=RECT_GATE_METRIC, d_c=512),
     # The large-N evaluation forward (noncausal_bias_mha via pallas_rectangular_edge_attention):
     # one system, all queries against all keys, dense [Nq, Nk, H] bias.
     "rect": Config("rect", 1, 4096, 16, 64, 4000, 0, "f32", 5,
@@ -570,6 +580,93 @@ def run_rect(args, cfg):
     return 0
 
 
+def run_rect_gate(args, cfg):
+    """Bench leg of the large-N attention tail (sequence_trunk.py:973-984): the rectangular
+    attention with the head collapse fused (hz_rect_attention_fwd_gated), then W_O with the
+    row mask (hz_gated_out_proj). The roofline is the gated attention kernel's, timed on its
+    own over the same number of launches."""
+    import torch
+
+    from hamiltonzero_amd import _native
+
+    lib = _native.lib()
+    dev = torch.device("cuda:0")
+    B, N, H, D, n_phys, d_c = cfg.B, cfg.N, cfg.H, cfg.D, cfg.n_phys, cfg.d_c
+    hh = H // 2
+    rng = np.random.default_rng(cfg.seed)
+
+    def draw(shape, scale):
+        return torch.from_numpy(rng.standard_normal(shape, dtype=np.float32) * np.float32(scale))
+
+    qh, kh, vh = draw((B, N, H, D), 1.0), draw((B, N, H, D), 1.0), draw((B, N, H, D), 1.0)
+    biash = draw((B, N, N, H), D ** -0.5)
+    w_oh = draw((hh * D, d_c), (hh * D) ** -0.5)
+    maskh = torch.zeros((B, N), dtype=torch.bool)
+    maskh[:, :n_phys] = True
+    q, k, v, bias, w_o = (x.to(dev) for x in (qh, kh, vh, biash, w_oh))
+    mask = maskh.to(torch.uint8).to(dev)
+    y = torch.empty((B, N, hh, D), dtype=torch.float32, device=dev)
+    proj = torch.empty((B, N, d_c), dtype=torch.float32, device=dev)
+    s = torch.cuda.current_stream(dev).cuda_stream
+    scale = D ** -0.5
+
+    def attend(i):
+        _native.check(lib.hz_rect_attention_fwd_gated(s, q.data_ptr(), k.data_ptr(), v.data_ptr(), bias.data_ptr(),
+                                                      mask.data_ptr(), y.data_ptr(), B, N, N, H, D, scale))
+
+    def project(i):
+        _native.check(lib.hz_gated_out_proj(s, y.data_ptr(), None, w_o.data_ptr(), mask.data_ptr(), proj.data_ptr(),
+                                            None, B, N, hh * D, d_c, 0))
+
+    def step(i):
+        attend(i)
+        project(i)
+
+    stream = torch.cuda.current_stream(dev)
+    ms = timed(step, args.steps, args.warmup, stream)
+    ms_att = timed(attend, args.steps, args.warmup, stream)
+    ms_proj = timed(project, args.steps, args.warmup, stream)
+    t_s = ms / 1e3
+    # the gated kernel: q, k, v, the bias and y once; 4 Nq Nk D flops per (system, head)
+    att_pad = dict(bytes=B * (N * H * D * 4 * 3 + N * N * H * 4 + N * hh * D * 4 + N), flops=B * H * 4 * N * N * D)
+    att_eff = dict(bytes=B * (N * H * D * 4 + 2 * n_phys * H * D * 4 + N * n_phys * H * 4 + N * hh * D * 4 + N),
+                   flops=B * H * 4 * N * n_phys * D)
+    roof = roofline(att_pad["bytes"], att_pad["flops"], ms_att / 1e3, "f32")
+    roof.update({"kernel": "rect_attention_fwd_kernel (gated)", "traffic": traffic_from_profile(args.config),
+                 "basis": "padded algorithmic bytes/flops of the gated attention kernel (q, k, v, bias, y once)",
+                 "bytes_per_launch": att_pad["bytes"], "flops_per_launch": att_pad["flops"],
+                 "step": {"attention_ms": ms_att, "out_proj_ms": ms_proj,
+                          "out_proj_flops": 2 * B * n_phys * hh * D * d_c}})
+    roof_mask = roofline(att_eff["bytes"], att_eff["flops"], ms_att / 1e3, "f32")
+    roof_mask["basis"] = "mask-aware (physical keys' k, v, bias columns and flops only)"
+    cpu = None
+    if not args.no_cpu_baseline:
+        from oracle import cpu_baseline
+
+        sample = 64
+        r = cpu_baseline.time_rect_block_queries_per_s(qh[:, :sample], kh, vh, biash[:, :sample], maskh, scale,
+                                                       w_oh, maskh[:, :sample], budget_s=args.cpu_budget)
+        err_y = rel_err(y[:, :sample].cpu().numpy(), r["y"].numpy())
+        err_p = rel_err(proj[:, :sample].cpu().numpy(), r["proj"].numpy())
+        cpu = {"value": r["queries_per_s"], "unit": "queries/s", "cores": r["threads"], "kind": "port",
+               "sample": f"the first {sample} query rows of the same system against all {N} keys, {r['reps']} reps "
+                         f"in {r['seconds']:.1f} s, torch-CPU fp32 port (attention, collapse, W_O) ({r['cpu_model']})",
+               "host_cpus": r["host_cpus"],
+               "check": {"max_rel_err_vs_gpu": {"y": err_y, "proj": err_p}, "tol": 1e-5,
+                         "ok": err_y <= 1e-5 and err_p <= 1e-5}}
+    line = {
+        "metric": cfg.metric, "value": B * N / t_s, "unit": "queries/s", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "settle_ms": args.settle_ms, "ms_per_step": ms, "higher_is_better": True,
+        "scaling": "weak", "vs_baseline": None, "dtype": "f32",
+        "data": "synthetic (numpy default_rng, N(0,1) q/k/v, N(0,1)/sqrt(D) bias, N(0,1)/sqrt(fan_in) W_O)",
+        "config": {"workload": f"{args.config}: {cfg.desc}", "B": B, "Nq": N, "Nk": N, "H": H, "D": D,
+                   "n_phys": n_phys, "d_c": d_c},
+        "roofline": roof, "roofline_mask_aware": roof_mask, "cpu_baseline": cpu,
+    }
+    print(json.dumps(line), flush=True)
+    return 0
+
+
 def run_executor(args, cfg):
     """Bench leg of one compiled-executor tree level (hz_quadrilinear_merge, hz_factorized_apply).
     Config fields: B walkers, N node pairs (width), H groups, D rank d_r, n_phys merge_rank."""
@@ -887,6 +984,8 @@ def main(argv=None):
     cfg = CONFIGS[args.config]
     if cfg.work == "rect":
         return run_rect(args, cfg)
+    if cfg.work == "rect_gate":
+        return run_rect_gate(args, cfg)
     if cfg.work == "executor":
         return run_executor(args, cfg)
     if cfg.work == "trunk":

@@ -10,7 +10,9 @@ Public surface, named after the reference modules it replaces:
   (``src/hamiltonzero/model/trunk.py``).
 * :mod:`hamiltonzero_amd.rect_attention` — ``noncausal_bias_mha`` and
   ``pallas_rectangular_edge_attention`` (``src/hamiltonzero/evaluation/pallas_mha.py``,
-  ``src/hamiltonzero/evaluation/sequence_parallel.py``), the large-N evaluation forward.
+  ``src/hamiltonzero/evaluation/sequence_parallel.py``), the large-N evaluation forward, and
+  the large-N caller's head collapse fused into it (``gated_rectangular_edge_attention``,
+  ``sequence_attention_output``: ``src/hamiltonzero/evaluation/sequence_trunk.py``).
 * :mod:`hamiltonzero_amd.kernels` — tensor-level calls of the C ABI
   (``include/hz_mhsea.h``): forward, tangent, fused forward+tangent, backward,
   gated forward+tangent, rectangular forward.
@@ -26,11 +28,18 @@ from .mhsea_tuned import (
     mhsea_tuned_jvp,
     mhsea_with_tuned_ad,
 )
-from .rect_attention import BlockSizes, noncausal_bias_mha, pallas_rectangular_edge_attention
+from .rect_attention import (
+    BlockSizes,
+    gated_rectangular_edge_attention,
+    noncausal_bias_mha,
+    pallas_rectangular_edge_attention,
+    sequence_attention_output,
+)
 
 __all__ = [
     "BlockSizes",
     "gated_edge_attention",
+    "gated_rectangular_edge_attention",
     "mhsea_ad",
     "mhsea_tuned_ad",
     "mhsea_tuned_ad_lin",
@@ -41,4 +50,5 @@ __all__ = [
     "noncausal_bias_mha",
     "pallas_rectangular_edge_attention",
     "reference_edge_attention",
+    "sequence_attention_output",
 ]

@@ -38,6 +38,7 @@ EXPORTED_SYMBOLS = (
     "hz_gated_out_proj",
     "hz_mhsea_bwd_gated",
     "hz_rect_attention_fwd",
+    "hz_rect_attention_fwd_gated",
     "hz_quadrilinear_merge",
     "hz_factorized_apply",
     "hz_factorized_apply_noalloc",
@@ -94,6 +95,8 @@ _SIGNATURES = {
     ),
     # stream, q, k, v, bias, key_mask, out, B, Nq, Nk, H, D, scale
     "hz_rect_attention_fwd": ([_P, _P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _F], _INT),
+    # stream, q, k, v, bias, key_mask, y, B, Nq, Nk, H, D, scale
+    "hz_rect_attention_fwd_gated": ([_P, _P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _F], _INT),
     # stream, T, u_a, u_b, out, M, G, R
     "hz_quadrilinear_merge": ([_P, _P, _P, _P, _P, _I64, _I64, _I64], _INT),
     # stream, x, V, h, U, residual, y, workspace, M, d_in, R, d_out, h_rows

@@ -152,6 +152,46 @@ int keymask_empty_fwd(const hz::FwdParams& p, int64_t D, int64_t T, bool given_l
   return launched(hz::launch_keymask_empty_fwd(p, static_cast<int>(D), static_cast<int>(T), given_lse, dtype, stream));
 }
 
+// Shared by the rectangular entry points: shape checks of noncausal_bias_mha
+// (pallas_mha.py:101-118) and _validate_rectangular_attention_inputs
+// (sequence_parallel.py:13-47), on C sizes, then the launch.
+int rect_attention(hipStream_t stream, const float* q, const float* k, const float* v, const float* bias,
+                   const uint8_t* key_mask, float* out, int64_t B, int64_t Nq, int64_t Nk, int64_t H, int64_t D,
+                   float scale, bool gated) {
+  if (B < 1 || H < 1) return fail(HZ_EINVAL, "B and H must be >= 1, got B=%lld H=%lld", (long long)B, (long long)H);
+  if (Nq < 1 || Nk < 1)
+    return fail(HZ_EINVAL, "query and key sequence lengths must both be positive, got Nq=%lld Nk=%lld",
+                (long long)Nq, (long long)Nk);
+  if (Nq > HZ_MAX_N || Nk > HZ_MAX_N)
+    return fail(HZ_EINVAL, "Nq and Nk must be <= %d, got Nq=%lld Nk=%lld", HZ_MAX_N, (long long)Nq, (long long)Nk);
+  if (D != 8 && D != 16 && D != 32 && D != 64)
+    return fail(HZ_EINVAL, "head dimension must be one of [8, 16, 32, 64], got %lld", (long long)D);
+  if (B * ((Nq + 63) / 64) * H > 0x7fffffffLL) return fail(HZ_EINVAL, "B*ceil(Nq/64)*H exceeds the grid limit");
+  if (B * Nk > 0x7fffffffLL) return fail(HZ_EINVAL, "B*Nk = %lld exceeds the supported mask size", (long long)(B * Nk));
+  if (B * Nq * Nk * H > (int64_t(1) << 46))
+    return fail(HZ_EINVAL, "B*Nq*Nk*H = %lld exceeds the supported tensor size", (long long)(B * Nq * Nk * H));
+  HZ_REQUIRE(q);
+  HZ_REQUIRE(k);
+  HZ_REQUIRE(v);
+  HZ_REQUIRE(out);
+  HZ_OPTIONAL(bias);
+  if (!std::isfinite(scale)) return fail(HZ_EINVAL, "scale must be finite");
+  hz::RectParams p{};
+  p.q = q;
+  p.k = k;
+  p.v = v;
+  p.bias = bias;
+  p.key_mask = key_mask;
+  p.out = out;
+  p.B = static_cast<int>(B);
+  p.Nq = static_cast<int>(Nq);
+  p.Nk = static_cast<int>(Nk);
+  p.H = static_cast<int>(H);
+  p.scale = scale;
+  p.gated = gated ? 1 : 0;
+  return launched(hz::launch_rect_fwd(p, static_cast<int>(D), stream));
+}
+
 }  // namespace
 
 extern "C" {
@@ -343,39 +383,15 @@ int hz_mhsea_bwd(hipStream_t stream, const void* q, const void* k, const void* e
 int hz_rect_attention_fwd(hipStream_t stream, const float* q, const float* k, const float* v,
                           const float* bias, const uint8_t* key_mask, float* out, int64_t B,
                           int64_t Nq, int64_t Nk, int64_t H, int64_t D, float scale) {
-  // Shape checks of noncausal_bias_mha (pallas_mha.py:101-118) and
-  // _validate_rectangular_attention_inputs (sequence_parallel.py:13-47), on C sizes.
-  if (B < 1 || H < 1) return fail(HZ_EINVAL, "B and H must be >= 1, got B=%lld H=%lld", (long long)B, (long long)H);
-  if (Nq < 1 || Nk < 1)
-    return fail(HZ_EINVAL, "query and key sequence lengths must both be positive, got Nq=%lld Nk=%lld",
-                (long long)Nq, (long long)Nk);
-  if (Nq > HZ_MAX_N || Nk > HZ_MAX_N)
-    return fail(HZ_EINVAL, "Nq and Nk must be <= %d, got Nq=%lld Nk=%lld", HZ_MAX_N, (long long)Nq, (long long)Nk);
-  if (D != 8 && D != 16 && D != 32 && D != 64)
-    return fail(HZ_EINVAL, "head dimension must be one of [8, 16, 32, 64], got %lld", (long long)D);
-  if (B * ((Nq + 63) / 64) * H > 0x7fffffffLL) return fail(HZ_EINVAL, "B*ceil(Nq/64)*H exceeds the grid limit");
-  if (B * Nk > 0x7fffffffLL) return fail(HZ_EINVAL, "B*Nk = %lld exceeds the supported mask size", (long long)(B * Nk));
-  if (B * Nq * Nk * H > (int64_t(1) << 46))
-    return fail(HZ_EINVAL, "B*Nq*Nk*H = %lld exceeds the supported tensor size", (long long)(B * Nq * Nk * H));
-  HZ_REQUIRE(q);
-  HZ_REQUIRE(k);
-  HZ_REQUIRE(v);
-  HZ_REQUIRE(out);
-  HZ_OPTIONAL(bias);
-  if (!std::isfinite(scale)) return fail(HZ_EINVAL, "scale must be finite");
-  hz::RectParams p{};
-  p.q = q;
-  p.k = k;
-  p.v = v;
-  p.bias = bias;
-  p.key_mask = key_mask;
-  p.out = out;
-  p.B = static_cast<int>(B);
-  p.Nq = static_cast<int>(Nq);
-  p.Nk = static_cast<int>(Nk);
-  p.H = static_cast<int>(H);
-  p.scale = scale;
-  return launched(hz::launch_rect_fwd(p, static_cast<int>(D), stream));
+  return rect_attention(stream, q, k, v, bias, key_mask, out, B, Nq, Nk, H, D, scale, false);
+}
+
+int hz_rect_attention_fwd_gated(hipStream_t stream, const float* q, const float* k, const float* v,
+                                const float* bias, const uint8_t* key_mask, float* y, int64_t B,
+                                int64_t Nq, int64_t Nk, int64_t H, int64_t D, float scale) {
+  if (H % 2 != 0)
+    return fail(HZ_EINVAL, "the gated collapse pairs head h with h + H/2: H must be even, got %lld", (long long)H);
+  return rect_attention(stream, q, k, v, bias, key_mask, y, B, Nq, Nk, H, D, scale, true);
 }
 
 int hz_quadrilinear_merge(hipStream_t stream, const float* T, const float* u_a, const float* u_b, float* out,

@@ -200,12 +200,13 @@ struct RectParams {
   const float* v;      // [B, Nk, H, D]
   const float* bias;   // [B, Nq, Nk, H]; may be null (zero bias)
   const uint8_t* key_mask;  // [B, Nk]; may be null (every key physical)
-  float* out;          // [B, Nq, H, D]
+  float* out;          // [B, Nq, H, D]; gated: y [B, Nq, H / 2, D]
   int B, Nq, Nk, H;
   float scale;
+  int gated;           // 1: y = sigmoid(out[:, :, :H/2]) * out[:, :, H/2:] instead of out
 };
 hipError_t launch_rect_fwd(const RectParams& p, int D, hipStream_t stream);
 // Dynamic LDS the rectangular kernel needs (largest variant for this D, H).
-size_t rect_fwd_lds_bytes(int D, int H, int Nk, bool masked);
+size_t rect_fwd_lds_bytes(int D, int H, int Nk, bool masked, bool gated);
 
 }  // namespace hz

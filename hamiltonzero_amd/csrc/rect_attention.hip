@@ -26,6 +26,12 @@
 // and S^T's output layout is directly the B operand of the P.V product. Keys (K and V of
 // the HG heads) and the bias block are staged in LDS in chunks of KC = 32 keys; the next
 // chunk is loaded into registers while the current one is computed.
+//
+// Gated mode (the large-N caller's head collapse, sequence_trunk.py:981): head h < H/2 gates
+// head h + H/2, y = sigmoid(out_h) * out_{h + H/2}, and only y [B, Nq, H/2, D] is written. A
+// workgroup then owns HG/2 consecutive gate heads g0.. and their value heads H/2 + g0..
+// (bias read as two HG/2-float vectors per (query, key)); after the key loop the gate waves
+// leave their normalised rows in LDS and the value wave of the same query tile combines them.
 #include <hip/hip_runtime.h>
 
 #include "mhsea_device.h"
@@ -60,6 +66,14 @@ struct RectShape {
   }
 };
 
+// Global head of local head hh of head group gi: HG consecutive heads, or (gated) HG/2 gate
+// heads and their HG/2 value heads H/2 further on.
+template <int HG, bool GATED>
+__device__ __forceinline__ int rect_head(int gi, int hh, int H) {
+  if constexpr (GATED) return hh < HG / 2 ? gi * (HG / 2) + hh : H / 2 + gi * (HG / 2) + (hh - HG / 2);
+  return gi * HG + hh;
+}
+
 // HG consecutive floats (the workgroup's heads of one bias element).
 template <int HG>
 struct BiasVec;
@@ -80,6 +94,24 @@ struct BiasVec<1> {
   float v;
   __device__ __forceinline__ void load(const float* p) { v = *p; }
   __device__ __forceinline__ float get(int) const { return v; }
+};
+
+// The workgroup's HG bias values of one (query, key): one HG-float vector, or (gated) the
+// HG/2 gate heads' and the HG/2 value heads' vectors.
+template <int HG, bool GATED>
+struct BiasHeads {
+  BiasVec<HG> v;
+  __device__ __forceinline__ void load(const float* row, int gi, int H) { v.load(row + gi * HG); }
+  __device__ __forceinline__ float get(int i) const { return v.get(i); }
+};
+template <int HG>
+struct BiasHeads<HG, true> {
+  BiasVec<HG / 2> gv, vv;
+  __device__ __forceinline__ void load(const float* row, int gi, int H) {
+    gv.load(row + gi * (HG / 2));
+    vv.load(row + H / 2 + gi * (HG / 2));
+  }
+  __device__ __forceinline__ float get(int i) const { return i < HG / 2 ? gv.get(i) : vv.get(i - HG / 2); }
 };
 
 // Compaction of one system's key mask into the ascending list of physical keys, for a
@@ -113,21 +145,21 @@ __device__ __forceinline__ int compact_keys(const uint8_t* __restrict__ mask_row
 
 // What the staging steps of one workgroup need (fixed for the whole kernel).
 struct StageArgs {
-  const float* kbase;  // k of this system at head h0
+  const float* kbase;  // k of this system (head 0)
   const float* vbase;
-  const float* ebase;  // bias of this system at head h0; null = no bias
+  const float* ebase;  // bias of this system (head 0); null = no bias
   const int16_t* idx;  // physical keys (LDS), used when gather
-  int nk, Nq, Nk, H, q0;
+  int nk, Nq, Nk, H, q0, gi;
   bool gather;
 };
 
 // Issue the global loads of key chunk [kc, kc + KC) into registers: the K and V rows of
-// the workgroup's HG heads (one contiguous HG*D run per key) and the bias block
-// [QB queries][KC keys][HG heads]. Every load is in bounds (padding rows read key 0 /
-// the last query row); padding is zeroed or ignored when the chunk is written to LDS.
-template <int D, int HG, int QT, int KVP, int BP>
-__device__ __forceinline__ void rect_load_chunk(float4 (&rk)[KVP], float4 (&rv)[KVP], BiasVec<HG> (&re)[BP],
-                                                const StageArgs& a, int kc) {
+// the workgroup's HG heads (one contiguous HG*D run per key, two runs when gated) and the
+// bias block [QB queries][KC keys][HG heads]. Every load is in bounds (padding rows read
+// key 0 / the last query row); padding is zeroed or ignored when the chunk is written to LDS.
+template <int D, int HG, int QT, bool GATED, int KVP, int BP>
+__device__ __forceinline__ void rect_load_chunk(float4 (&rk)[KVP], float4 (&rv)[KVP],
+                                                BiasHeads<HG, GATED> (&re)[BP], const StageArgs& a, int kc) {
   using Sh = RectShape<D, HG, QT>;
   const int tid = threadIdx.x;
 #pragma unroll
@@ -136,7 +168,9 @@ __device__ __forceinline__ void rect_load_chunk(float4 (&rk)[KVP], float4 (&rv)[
     const int j = kc + it / Sh::kRowItems;
     const bool ok = (Sh::kKvItems % Sh::NT == 0 || it < Sh::kKvItems) && j < a.nk;
     const int n = ok ? (a.gather ? a.idx[j] : j) : 0;
-    const int64_t off = static_cast<int64_t>(n) * a.H * D + (it % Sh::kRowItems) * 4;
+    const int hh = (it % Sh::kRowItems) / Sh::C4;
+    const int64_t off = static_cast<int64_t>(n) * a.H * D + rect_head<HG, GATED>(a.gi, hh, a.H) * D +
+                        (it % Sh::C4) * 4;
     rk[u] = *reinterpret_cast<const float4*>(a.kbase + off);
     rv[u] = *reinterpret_cast<const float4*>(a.vbase + off);
   }
@@ -148,17 +182,17 @@ __device__ __forceinline__ void rect_load_chunk(float4 (&rk)[KVP], float4 (&rv)[
       const int j = kc + it % Sh::KC;
       const int qrow = a.q0 + qi < a.Nq ? a.q0 + qi : a.Nq - 1;
       const int n = j < a.nk ? (a.gather ? a.idx[j] : j) : 0;
-      re[u].load(a.ebase + (static_cast<int64_t>(qrow) * a.Nk + n) * a.H);
+      re[u].load(a.ebase + (static_cast<int64_t>(qrow) * a.Nk + n) * a.H, a.gi, a.H);
     }
   }
 }
 
 // Write the staged chunk to LDS: K and V as [head][key][LD] (rows past the last key
 // zeroed), the bias as [head][query][KCP].
-template <int D, int HG, int QT, int KVP, int BP>
+template <int D, int HG, int QT, bool GATED, int KVP, int BP>
 __device__ __forceinline__ void rect_store_chunk(const float4 (&rk)[KVP], const float4 (&rv)[KVP],
-                                                 const BiasVec<HG> (&re)[BP], float* Ks, float* Vs, float* Es,
-                                                 const StageArgs& a, int kc) {
+                                                 const BiasHeads<HG, GATED> (&re)[BP], float* Ks, float* Vs,
+                                                 float* Es, const StageArgs& a, int kc) {
   using Sh = RectShape<D, HG, QT>;
   const int tid = threadIdx.x;
 #pragma unroll
@@ -190,7 +224,7 @@ __device__ __forceinline__ void rect_store_chunk(const float4 (&rk)[KVP], const 
   }
 }
 
-template <int D, int HG, int QT>
+template <int D, int HG, int QT, bool GATED>
 __global__ void __launch_bounds__(64 * QT * HG) rect_attention_fwd_kernel(const RectParams p) {
   using Sh = RectShape<D, HG, QT>;
   constexpr int KC = Sh::KC, NJT = Sh::NJT, LD = Sh::LD, KCP = Sh::KCP, QB = Sh::QB;
@@ -214,7 +248,6 @@ __global__ void __launch_bounds__(64 * QT * HG) rect_attention_fwd_kernel(const 
   const int hgi = static_cast<int>(lb % nhg);
   const int qblk = static_cast<int>((lb / nhg) % nqb);
   const int b = static_cast<int>(lb / (static_cast<int64_t>(nhg) * nqb));
-  const int h0 = hgi * HG;
   const int q0 = qblk * QB;
 
   const int tid = threadIdx.x;
@@ -241,19 +274,19 @@ __global__ void __launch_bounds__(64 * QT * HG) rect_attention_fwd_kernel(const 
 
   // ---- staging: registers <- global (next chunk), LDS <- registers (this chunk) ---------
   float4 rk[KVP], rv[KVP];
-  BiasVec<HG> re[BP];
-  const float* const kbase = p.k + static_cast<int64_t>(b) * Nk * H * D + h0 * D;
-  const float* const vbase = p.v + static_cast<int64_t>(b) * Nk * H * D + h0 * D;
-  const float* const ebase = p.bias == nullptr ? nullptr : p.bias + static_cast<int64_t>(b) * Nq * Nk * H + h0;
-  const StageArgs sa{kbase, vbase, ebase, idx, nk, Nq, Nk, H, q0, gather};
+  BiasHeads<HG, GATED> re[BP];
+  const float* const kbase = p.k + static_cast<int64_t>(b) * Nk * H * D;
+  const float* const vbase = p.v + static_cast<int64_t>(b) * Nk * H * D;
+  const float* const ebase = p.bias == nullptr ? nullptr : p.bias + static_cast<int64_t>(b) * Nq * Nk * H;
+  const StageArgs sa{kbase, vbase, ebase, idx, nk, Nq, Nk, H, q0, hgi, gather};
 
-  rect_load_chunk<D, HG, QT>(rk, rv, re, sa, 0);
+  rect_load_chunk<D, HG, QT, GATED>(rk, rv, re, sa, 0);
 
   // Query fragment in B-operand layout: lane (g, c) holds q[q][h][g*DG .. g*DG + DG), scaled.
   const int qrow = q0 + qt * 16 + c;
   const bool active = q0 + qt * 16 < Nq;  // wave-uniform
   const bool qvalid = qrow < Nq;
-  const int h = h0 + hl;
+  const int h = rect_head<HG, GATED>(hgi, hl, H);
   float qf[DG];
   {
     const int64_t qoff = ((static_cast<int64_t>(b) * Nq + (qvalid ? qrow : 0)) * H + h) * D + g * DG;
@@ -289,9 +322,9 @@ __global__ void __launch_bounds__(64 * QT * HG) rect_attention_fwd_kernel(const 
 
   for (int kc = 0; kc < nk; kc += KC) {
     if (kc > 0) __syncthreads();  // every wave is done with the previous chunk
-    rect_store_chunk<D, HG, QT>(rk, rv, re, Ks, Vs, Es, sa, kc);
+    rect_store_chunk<D, HG, QT, GATED>(rk, rv, re, Ks, Vs, Es, sa, kc);
     __syncthreads();
-    if (kc + KC < nk) rect_load_chunk<D, HG, QT>(rk, rv, re, sa, kc + KC);
+    if (kc + KC < nk) rect_load_chunk<D, HG, QT, GATED>(rk, rv, re, sa, kc + KC);
     if (!active) continue;
 
     // Scores of the chunk's key tiles, the tiles' accumulator chains interleaved (one
@@ -375,7 +408,40 @@ __global__ void __launch_bounds__(64 * QT * HG) rect_attention_fwd_kernel(const 
     }
   }
 
-  if (active) {
+  if constexpr (GATED) {
+    // Gate waves (local heads < HG/2) leave sigmoid(out) of their 16 queries in LDS (over
+    // the K chunk, free once every wave is past the key loop); the value wave of the same
+    // query tile multiplies it into its own rows and writes y.
+    constexpr int GLD = D + 4;
+    float* const Gs = Ks;  // [HG/2][QB][GLD] floats, within the K chunk region
+    static_assert((HG / 2) * QB * GLD <= Sh::kKvFloats, "gate rows must fit the K chunk region");
+    __syncthreads();
+    const float inv = active ? 1.f / group_sum(lsum) : 0.f;
+    float* const grow = Gs + ((hl % (HG / 2)) * QB + qt * 16 + c) * GLD;
+    if (hl < HG / 2 && active) {
+#pragma unroll
+      for (int dt = 0; dt < DT; ++dt) {
+        const int d0 = dt * 16 + 4 * g;
+        if (D % 16 != 0 && d0 >= D) continue;
+        float sg[4];
+#pragma unroll
+        for (int r = 0; r < 4; ++r) sg[r] = __builtin_amdgcn_rcpf(1.f + fast_exp2(-kLog2e * (o[dt][r] * inv)));
+        *reinterpret_cast<float4*>(grow + d0) = make_float4(sg[0], sg[1], sg[2], sg[3]);
+      }
+    }
+    __syncthreads();
+    if (hl >= HG / 2 && active && qvalid) {
+      float* const yrow = p.out + ((static_cast<int64_t>(b) * Nq + qrow) * (H / 2) + (h - H / 2)) * D;
+#pragma unroll
+      for (int dt = 0; dt < DT; ++dt) {
+        const int d0 = dt * 16 + 4 * g;
+        if (D % 16 != 0 && d0 >= D) continue;
+        const float4 sg = *reinterpret_cast<const float4*>(grow + d0);
+        *reinterpret_cast<float4*>(yrow + d0) = make_float4(sg.x * (o[dt][0] * inv), sg.y * (o[dt][1] * inv),
+                                                            sg.z * (o[dt][2] * inv), sg.w * (o[dt][3] * inv));
+      }
+    }
+  } else if (active) {
     // The cross-lane reduction runs on the whole wave; only the stores are per lane.
     const float inv = 1.f / group_sum(lsum);
     if (qvalid) {
@@ -391,12 +457,12 @@ __global__ void __launch_bounds__(64 * QT * HG) rect_attention_fwd_kernel(const 
   }
 }
 
-template <int D, int HG, int QT>
+template <int D, int HG, int QT, bool GATED>
 hipError_t launch_rect_t(const RectParams& p, hipStream_t stream) {
   using Sh = RectShape<D, HG, QT>;
   const int64_t nwg = static_cast<int64_t>(p.B) * ((p.Nq + Sh::QB - 1) / Sh::QB) * (p.H / HG);
   const size_t lds = Sh::lds_bytes(p.Nk, p.key_mask != nullptr);
-  auto kern = rect_attention_fwd_kernel<D, HG, QT>;
+  auto kern = rect_attention_fwd_kernel<D, HG, QT, GATED>;
   hipError_t err = hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
                                        hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(lds));
   if (err != hipSuccess) return err;
@@ -404,20 +470,26 @@ hipError_t launch_rect_t(const RectParams& p, hipStream_t stream) {
   return hipGetLastError();
 }
 
-template <int D, int HG>
+template <int D, int HG, bool GATED>
 hipError_t launch_rect_hg(const RectParams& p, hipStream_t stream) {
   // Four query tiles per workgroup share each staged K / V chunk; fall back to one tile
   // when that would leave CUs idle (fewer than 256 workgroups).
   const int64_t big = static_cast<int64_t>(p.B) * ((p.Nq + 63) / 64) * (p.H / HG);
-  if (big >= 256) return launch_rect_t<D, HG, 4>(p, stream);
-  return launch_rect_t<D, HG, 1>(p, stream);
+  if (big >= 256) return launch_rect_t<D, HG, 4, GATED>(p, stream);
+  return launch_rect_t<D, HG, 1, GATED>(p, stream);
 }
 
 template <int D>
 hipError_t launch_rect_d(const RectParams& p, hipStream_t stream) {
-  if (p.H % 4 == 0) return launch_rect_hg<D, 4>(p, stream);
-  if (p.H % 2 == 0) return launch_rect_hg<D, 2>(p, stream);
-  return launch_rect_hg<D, 1>(p, stream);
+  if (p.gated) {
+    // head groups of HG/2 gate heads and their value heads: HG/2 must divide H/2
+    if (p.H % 2 != 0) return hipErrorInvalidValue;
+    if ((p.H / 2) % 2 == 0) return launch_rect_hg<D, 4, true>(p, stream);
+    return launch_rect_hg<D, 2, true>(p, stream);
+  }
+  if (p.H % 4 == 0) return launch_rect_hg<D, 4, false>(p, stream);
+  if (p.H % 2 == 0) return launch_rect_hg<D, 2, false>(p, stream);
+  return launch_rect_hg<D, 1, false>(p, stream);
 }
 
 }  // namespace
@@ -437,8 +509,8 @@ hipError_t launch_rect_fwd(const RectParams& p, int D, hipStream_t stream) {
   }
 }
 
-size_t rect_fwd_lds_bytes(int D, int H, int Nk, bool masked) {
-  const int hg = H % 4 == 0 ? 4 : (H % 2 == 0 ? 2 : 1);
+size_t rect_fwd_lds_bytes(int D, int H, int Nk, bool masked, bool gated) {
+  const int hg = gated ? ((H / 2) % 2 == 0 ? 4 : 2) : (H % 4 == 0 ? 4 : (H % 2 == 0 ? 2 : 1));
   // The largest variant (four query tiles) bounds the requirement.
   switch (D * 8 + hg) {
 #define HZ_RECT_CASE(d, g) \

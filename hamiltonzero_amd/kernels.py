@@ -409,12 +409,15 @@ def rect_attention_fwd(
     bias: Optional[Tensor] = None,
     key_mask: Optional[Tensor] = None,
     scale: float = 1.0,
+    gated: bool = False,
 ) -> Tensor:
     """Rectangular attention with a dense pair bias (``hz_rect_attention_fwd``).
 
     ``q [B, Nq, H, D]``, ``k, v [B, Nk, H, D]``, ``bias [B, Nq, Nk, H]`` (None: zero),
     ``key_mask [B, Nk]`` (None: every key); float32. Returns ``out [B, Nq, H, D]`` of
-    ``softmax_j(scale q.k + where(key_mask, bias, -1e30)) v``.
+    ``softmax_j(scale q.k + where(key_mask, bias, -1e30)) v``, or with ``gated`` only the
+    head collapse ``y [B, Nq, H/2, D] = sigmoid(out[:, :, :H/2]) * out[:, :, H/2:]``
+    (``hz_rect_attention_fwd_gated``).
     """
     if q.dim() != 4 or k.dim() != 4 or v.dim() != 4:
         raise ValueError("q, k and v must have rank 4 [B, N, H, D]")
@@ -435,12 +438,13 @@ def rect_attention_fwd(
         raise ValueError(f"key_mask must have shape {(B, Nk)}, got {tuple(key_mask.shape)}")
     _on_device(q.device, k=k, v=v, bias=bias)
     q, k, v, bias = map(_c, (q, k, v, bias))
+    if gated and H % 2 != 0:
+        raise ValueError(f"the gated collapse pairs head h with h + H/2: H must be even, got {H}")
     m = None if key_mask is None else _mask_u8(key_mask, q.device)
-    out = torch.empty_like(q)
+    out = torch.empty((B, Nq, H // 2, D) if gated else (B, Nq, H, D), dtype=q.dtype, device=q.device)
+    fn = _native.lib().hz_rect_attention_fwd_gated if gated else _native.lib().hz_rect_attention_fwd
     _native.check(
-        _native.lib().hz_rect_attention_fwd(
-            _stream(q.device), _ptr(q), _ptr(k), _ptr(v), _ptr(bias), _ptr(m), _ptr(out),
-            B, Nq, Nk, H, D, float(scale),
-        )
+        fn(_stream(q.device), _ptr(q), _ptr(k), _ptr(v), _ptr(bias), _ptr(m), _ptr(out), B, Nq, Nk, H, D,
+           float(scale))
     )
     return out

@@ -122,4 +122,50 @@ def pallas_rectangular_edge_attention(
     return out[0]
 
 
-__all__ = ["BlockSizes", "noncausal_bias_mha", "pallas_rectangular_edge_attention"]
+def gated_rectangular_edge_attention(
+    q_local: Tensor,
+    k_global: Tensor,
+    v_global: Tensor,
+    edge_bias_local: Tensor,
+    key_mask: Tensor,
+    *,
+    block_k: int | None = None,
+) -> Tensor:
+    """The large-N caller's attention and head collapse in one kernel
+    (``_sequence_level_edge_attention``, sequence_trunk.py:973-981):
+    ``sigmoid(out[:, :h/2]) * out[:, h/2:]`` of :func:`pallas_rectangular_edge_attention`'s
+    ``out``, with the same operands and checks. Returns ``[r, h/2, d]``; the attention
+    output itself is never written."""
+    _validate_rectangular_attention_inputs(q_local, k_global, v_global, edge_bias_local, key_mask)
+    sm_scale = float(q_local.shape[-1]) ** -0.5
+    _dividing_block_size(q_local.shape[0], None)
+    _dividing_block_size(k_global.shape[0], block_k)
+    y = kernels.rect_attention_fwd(
+        q_local[None], k_global[None], v_global[None], edge_bias_local[None], key_mask[None], scale=sm_scale,
+        gated=True,
+    )
+    return y[0]
+
+
+def sequence_attention_output(
+    q_local: Tensor,
+    k_global: Tensor,
+    v_global: Tensor,
+    edge_bias_local: Tensor,
+    key_mask: Tensor,
+    w_o: Tensor,
+    row_mask: Tensor,
+    *,
+    block_k: int | None = None,
+) -> Tensor:
+    """``proposal_attn = row_mask[:, None] * (y.reshape(r, -1) @ w_o)`` with ``y`` from
+    :func:`gated_rectangular_edge_attention` (sequence_trunk.py:973-984): two launches, the
+    gated attention and the site-masked W_O (rows with ``row_mask`` 0 are written as zeros
+    without being multiplied). ``w_o [h/2 * d, d_c]``, ``row_mask [r]``; returns ``[r, d_c]``."""
+    y = gated_rectangular_edge_attention(q_local, k_global, v_global, edge_bias_local, key_mask, block_k=block_k)
+    delta, _ = kernels.gated_out_proj(y[None], w_o, mask=row_mask[None])
+    return delta[0]
+
+
+__all__ = ["BlockSizes", "gated_rectangular_edge_attention", "noncausal_bias_mha", "pallas_rectangular_edge_attention",
+           "sequence_attention_output"]

@@ -234,6 +234,23 @@ int hz_rect_attention_fwd(hipStream_t stream,
                           int64_t B, int64_t Nq, int64_t Nk, int64_t H, int64_t D,
                           float scale);
 
+/*
+ * hz_rect_attention_fwd with the large-N caller's head collapse fused into its epilogue.
+ * Replaces, in _sequence_level_edge_attention (src/hamiltonzero/evaluation/
+ * sequence_trunk.py:973-981), pallas_rectangular_edge_attention followed by
+ *     out = sigmoid(out[:, :n_heads]) * out[:, n_heads:]
+ * (n_heads = H / 2, the kernel's H = 2 n_heads heads): writes only
+ *     y [B, Nq, H/2, D] = sigmoid(out[:, :, :H/2]) * out[:, :, H/2:]
+ * with out as hz_rect_attention_fwd defines it (same operands, layouts, mask and scale);
+ * the attention output itself never reaches memory. H must be even. The caller's W_O with
+ * the row mask (sequence_trunk.py:982-984) is hz_gated_out_proj on y.
+ */
+int hz_rect_attention_fwd_gated(hipStream_t stream,
+                                const float* q, const float* k, const float* v,
+                                const float* bias, const uint8_t* key_mask, float* y,
+                                int64_t B, int64_t Nq, int64_t Nk, int64_t H, int64_t D,
+                                float scale);
+
 #ifdef __cplusplus
 }
 #endif

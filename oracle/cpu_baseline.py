@@ -200,6 +200,44 @@ def time_rect_queries_per_s(q, k, v, bias, key_mask, scale, budget_s: float = 15
     }
 
 
+def rect_block(q, k, v, bias, key_mask, scale, w_o, row_mask):
+    """The large-N attention tail in torch-CPU float32 (sequence_trunk.py:973-984): the
+    rectangular attention, the head collapse sigmoid(out[:, :, :H/2]) * out[:, :, H/2:] and
+    row_mask * (y_flat @ w_o). Returns (y, proj)."""
+    out = rect_attention(q, k, v, bias, key_mask, scale)
+    hh = out.shape[2] // 2
+    y = torch.sigmoid(out[:, :, :hh]) * out[:, :, hh:]
+    proj = (y.reshape(y.shape[0], y.shape[1], -1) @ w_o) * row_mask[:, :, None].to(y.dtype)
+    return y, proj
+
+
+def time_rect_block_queries_per_s(q, k, v, bias, key_mask, scale, w_o, row_mask, budget_s: float = 15.0,
+                                  threads: int | None = None) -> dict:
+    """Time :func:`rect_block` for the query rows of ``q [1, Nq_sample, H, D]`` against all
+    keys; returns query rows per second and (y, proj) of the last repetition."""
+    threads = threads or default_threads()
+    torch.set_num_threads(threads)
+    with torch.no_grad():
+        res = rect_block(q, k, v, bias, key_mask, scale, w_o, row_mask)  # warm-up
+        reps, t0 = 0, time.perf_counter()
+        while True:
+            res = rect_block(q, k, v, bias, key_mask, scale, w_o, row_mask)
+            reps += 1
+            el = time.perf_counter() - t0
+            if el >= budget_s or reps >= 100000:
+                break
+    return {
+        "queries_per_s": q.shape[1] * reps / el,
+        "seconds": el,
+        "reps": reps,
+        "threads": threads,
+        "cpu_model": host_cpu_model(),
+        "host_cpus": host_cpus(),
+        "y": res[0],
+        "proj": res[1],
+    }
+
+
 def executor_level(T, ul, ur, V, U, h):
     """One compiled-executor level's products in torch-CPU float32: the quadrilinear merge
     (einsum, _custom_lap_primitives.py:45-50) and the residual factorized apply

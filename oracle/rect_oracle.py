@@ -27,7 +27,10 @@ values); the all-masked mean; equality with the already-pinned square oracle
 the sequence-parallel identity (a block of query rows of the square problem equals the
 rectangular problem on that block); invariance under a permutation of the keys and under
 any finite change of masked keys' k and v and any change (NaN included) of their bias. Planted mistakes (bias read
-transposed, mask ignored, scale on k only) fail these checks.
+transposed, mask ignored, scale on k only) fail these checks. ``rect_gated`` and
+``sequence_attention_output`` compose ``rect_fwd`` with ``mhsea_oracle.gate_collapse`` and
+``mhsea_oracle.out_proj`` (pinned in tests/test_gated_oracle.py); tests/test_rect_oracle.py
+checks the composition against element loops, including the head pairing.
 """
 
 from __future__ import annotations
@@ -65,6 +68,23 @@ def rect_fwd(q, k, v, bias=None, key_mask=None, *, scale=1.0):
     # masked keys have weight exp(-1e30 - m) = 0 (as in the reference, a non-finite k or v
     # of a masked key would still propagate through q.k and 0 * v)
     return np.einsum("bhij,bjhd->bihd", p, v)
+
+
+def rect_gated(q, k, v, bias=None, key_mask=None, *, scale=1.0):
+    """y [B, Nq, H/2, D]: the large-N caller's head collapse after the rectangular attention,
+    ``sigmoid(out[:, :, :H/2]) * out[:, :, H/2:]`` (``sequence_trunk.py:973-981``; the
+    kernel's H is twice the module's n_heads), with ``out`` from :func:`rect_fwd`."""
+    from .mhsea_oracle import gate_collapse
+
+    return gate_collapse(rect_fwd(q, k, v, bias, key_mask, scale=scale))
+
+
+def sequence_attention_output(q, k, v, bias, key_mask, w_o, row_mask, *, scale=1.0):
+    """``row_mask[:, None] * (y.reshape(r, -1) @ w_o)`` per system (``sequence_trunk.py:
+    982-984``), y from :func:`rect_gated`. w_o [H/2 * D, d_c], row_mask [B, Nq]."""
+    from .mhsea_oracle import out_proj
+
+    return out_proj(rect_gated(q, k, v, bias, key_mask, scale=scale), w_o, row_mask)
 
 
 def rect_fwd_loops(q, k, v, bias, key_mask, *, scale=1.0):

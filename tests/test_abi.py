@@ -147,6 +147,16 @@ def test_rect_rejects_bad_arguments(lib):
         assert call(**over) == code, over
         assert needle in lib.hz_last_error().decode(), over
     assert len(lib.hz_rect_attention_fwd.argtypes) == 13
+    # the gated variant: the same checks, and an even head count
+    gated = lib.hz_rect_attention_fwd_gated
+    assert len(gated.argtypes) == 13
+    for over, code, needle in cases + [(dict(H=15), _native.HZ_EINVAL, "H must be even")]:
+        args = list(base)
+        names = ["stream", "q", "k", "v", "bias", "key_mask", "out", "B", "Nq", "Nk", "H", "D", "scale"]
+        for key, val in over.items():
+            args[names.index(key)] = val
+        assert gated(*args) == code, over
+        assert needle in lib.hz_last_error().decode(), over
 
 
 def test_gated_rejects_bad_arguments(lib):

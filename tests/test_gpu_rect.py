@@ -131,3 +131,64 @@ def test_reference_named_wrappers():
     out = RA.noncausal_bias_mha(dev(q), dev(k), dev(v), dev(e))
     torch.cuda.synchronize()
     assert rel(out.cpu().numpy(), R.rect_fwd(q, k, v, e, None, scale=1.0)) <= F32_TOL
+
+
+GATED_CASES = [
+    # B, Nq, Nk, H, D, n_phys, scattered, bias
+    (1, 64, 64, 4, 32, None, False, True),       # H/2 even: two gate + two value heads per workgroup
+    (2, 100, 75, 8, 64, 60, True, True),
+    (1, 256, 1024, 16, 64, 1000, False, True),   # the large-N shape, four query tiles per workgroup
+    (3, 33, 47, 6, 16, 20, True, True),          # H/2 odd: one gate + one value head per workgroup
+    (2, 17, 40, 2, 8, -1, True, True),           # a single head pair, per-system key counts
+    (4, 128, 96, 8, 16, 80, True, False),        # no bias
+    (2, 96, 130, 4, 64, 0, False, True),         # every key masked
+    (1, 300, 33, 16, 32, None, False, True),
+]
+
+
+@pytest.mark.parametrize("case", GATED_CASES, ids=lambda c: "B%d_Nq%d_Nk%d_H%d_D%d_n%s_%s_%s" % (
+    c[0], c[1], c[2], c[3], c[4], c[5], "scat" if c[6] else "pre", "bias" if c[7] else "nobias"))
+def test_rect_gated_parity(case):
+    """hz_rect_attention_fwd_gated: y = sigmoid(out[:, :, :H/2]) * out[:, :, H/2:] against the
+    oracle, and against the ungated kernel followed by the collapse in torch."""
+    from hamiltonzero_amd import kernels
+
+    B, Nq, Nk, H, D, n_phys, scattered, bias = case
+    _say(f"rect gated B={B} Nq={Nq} Nk={Nk} H={H} D={D} n_phys={n_phys} scattered={scattered} bias={bias}")
+    q, k, v, e, mask = make(2000 + Nq + Nk + H + D, B, Nq, Nk, H, D, n_phys, scattered, bias)
+    scale = D ** -0.5
+    y = kernels.rect_attention_fwd(dev(q), dev(k), dev(v), dev(e), dev(mask), scale=scale, gated=True)
+    out = kernels.rect_attention_fwd(dev(q), dev(k), dev(v), dev(e), dev(mask), scale=scale)
+    torch.cuda.synchronize()
+    assert tuple(y.shape) == (B, Nq, H // 2, D)
+    assert rel(y.cpu().numpy(), R.rect_gated(q, k, v, e, mask, scale=scale)) <= F32_TOL
+    unfused = torch.sigmoid(out[:, :, : H // 2]) * out[:, :, H // 2:]
+    assert rel(y.cpu().numpy(), unfused.cpu().numpy()) <= F32_TOL
+
+
+def test_sequence_attention_output():
+    """The large-N attention tail (sequence_trunk.py:973-984) through the mirror: gated
+    rectangular attention, then W_O with the row mask, on one system; masked rows zero."""
+    from hamiltonzero_amd import rect_attention as RA
+
+    _say("rect gated + W_O mirror")
+    rng = np.random.default_rng(12)
+    q, k, v, e, mask = make(13, 1, 192, 256, 16, 16, n_phys=240, scattered=True)
+    w_o = (rng.standard_normal((8 * 16, 64)) / np.sqrt(128)).astype(np.float32)
+    row_mask = rng.random((1, 192)) < 0.7
+    got = RA.sequence_attention_output(dev(q[0]), dev(k[0]), dev(v[0]), dev(e[0]), dev(mask[0]), dev(w_o),
+                                       dev(row_mask[0]))
+    y = RA.gated_rectangular_edge_attention(dev(q[0]), dev(k[0]), dev(v[0]), dev(e[0]), dev(mask[0]))
+    torch.cuda.synchronize()
+    want = R.sequence_attention_output(q, k, v, e, mask, w_o, row_mask, scale=16 ** -0.5)[0]
+    assert rel(got.cpu().numpy(), want) <= F32_TOL
+    assert np.all(got.cpu().numpy()[~row_mask[0]] == 0.0)
+    assert rel(y.cpu().numpy(), R.rect_gated(q, k, v, e, mask, scale=16 ** -0.5)[0]) <= F32_TOL
+
+
+def test_rect_gated_rejects_odd_heads():
+    from hamiltonzero_amd import kernels
+
+    q, k, v, e, _ = make(14, 1, 16, 16, 3, 8)
+    with pytest.raises(ValueError, match="H must be even"):
+        kernels.rect_attention_fwd(dev(q), dev(k), dev(v), dev(e), None, gated=True)

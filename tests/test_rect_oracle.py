@@ -149,3 +149,44 @@ def test_planted_mistakes_are_caught(kind):
     bad = _planted(kind)(q, k, v, bias, mask, scale=0.5)
     want = R.rect_fwd_loops(q, k, v, bias, mask, scale=0.5)
     assert rel(bad, want) > 1e-3
+
+
+def _gated_loops(q, k, v, bias, mask, w_o, row_mask, scale):
+    """y and the masked projection by explicit loops over the element-loop forward: head h
+    of y is sigmoid(head h) times head h + H/2 (H/2 = the module's n_heads)."""
+    import math
+
+    out = R.rect_fwd_loops(q, k, v, bias, mask, scale=scale)
+    B, Nq, H, D = out.shape
+    hh = H // 2
+    y = np.zeros((B, Nq, hh, D))
+    for b in range(B):
+        for i in range(Nq):
+            for h in range(hh):
+                for d in range(D):
+                    y[b, i, h, d] = out[b, i, h + hh, d] / (1.0 + math.exp(-out[b, i, h, d]))
+    proj = np.zeros((B, Nq, w_o.shape[1]))
+    for b in range(B):
+        for i in range(Nq):
+            if not row_mask[b, i]:
+                continue
+            flat = y[b, i].reshape(-1)
+            for o in range(w_o.shape[1]):
+                proj[b, i, o] = sum(flat[f] * w_o[f, o] for f in range(flat.size))
+    return y, proj
+
+
+def test_gated_and_projection_against_loops():
+    """rect_gated / sequence_attention_output against explicit loops; swapping the gate and
+    value halves (a planted mistake) fails."""
+    rng = np.random.default_rng(9)
+    B, Nq, Nk, H, D = 2, 5, 7, 4, 8
+    q, k, v, bias, mask = make(rng, B, Nq, Nk, H, D, n_phys=5, scattered=True)
+    w_o = rng.standard_normal((H // 2 * D, 6))
+    row_mask = rng.random((B, Nq)) < 0.6
+    y_loop, proj_loop = _gated_loops(q, k, v, bias, mask, w_o, row_mask, 0.5)
+    assert rel(R.rect_gated(q, k, v, bias, mask, scale=0.5), y_loop) < 1e-12
+    assert rel(R.sequence_attention_output(q, k, v, bias, mask, w_o, row_mask, scale=0.5), proj_loop) < 1e-12
+    out = R.rect_fwd(q, k, v, bias, mask, scale=0.5)
+    swapped = out[:, :, : H // 2] / (1.0 + np.exp(-out[:, :, H // 2:]))  # gate and value exchanged
+    assert rel(swapped, y_loop) > 1e-3
