@@ -48,6 +48,8 @@ TRUNK_METRIC = ("trunk attention block after W_QKV (ln_edge + bias_mlp producer,
 VJP_METRIC = "fwd+VJP attention walkers/sec at B=1024,L=64 (fp32 training path); % of MFMA/HBM roofline"
 GATE_VJP_METRIC = ("fwd+VJP attention with the sigmoid-gate head collapse and the bias cotangent, walkers/sec at "
                    "B=1024,L=64; % of MFMA/HBM roofline")
+TREE_BIAS_METRIC = ("tree coupling-bias producer (normalised pair MLP + LCA-ALiBi, with tangent) walkers/sec at "
+                    "B=1024,L=64; % of MFMA roofline")
 HBM_PEAK_GBS = 8000.0
 FP32_PEAK_TFLOPS = 157.3
 BF16_PEAK_TFLOPS = 2516.6
@@ -151,6 +153,15 @@ CONFIGS = {
                         "large-N attention tail: rectangular attention with the gate collapse fused (one system, "
                         "Nq=Nk=4096, H=16 -> 8 gated heads, D=64, dense bias, 4000/4096 physical sites) -> y "
                         "[4096,8,64] -> W_O [512,512] on the physical rows", metric=RECT_GATE_METRIC, d_c=512),
+    # The tree's LevelEdgeAttn coupling bias (tree.py:1392-1456): the normalised MLP over the
+    # edge features (edge_channels 96 -> hidden 128 (level_edge_bias_mlp_dim) -> 16 heads, one
+    # block, config.py:25,82-83), / sqrt(d_head), + LCA-ALiBi, with its forward-mode tangent;
+    # D holds the hidden width and d_c the edge channels.
+    "tree_bias": Config("pair_mlp", 1024, 64, 16, 128, 36, 1, "f32", 9,
+                        "the tree's coupling-bias producer: edge [1024,64,64,96] and its tangent -> normalised MLP "
+                        "(96 -> 128, one block, -> 16 heads) / sqrt(16) + LCA-ALiBi -> e, e_t [1024,64,64,16], "
+                        "36/64 physical sites (square mask: the 36 x 36 pairs the attention reads)", cpu_sample=8,
+                        metric=TREE_BIAS_METRIC, d_c=96),
     # The large-N evaluation forward (noncausal_bias_mha via pallas_rectangular_edge_attention):
     # one system, all queries against all keys, dense [Nq, Nk, H] bias.
     "rect": Config("rect", 1, 4096, 16, 64, 4000, 0, "f32", 5,
@@ -667,6 +678,88 @@ def run_rect_gate(args, cfg):
     return 0
 
 
+def run_pair_mlp(args, cfg):
+    """Bench leg of the MLP-class bias producer (hz_pair_mlp_bias) at the tree's shape: edge
+    [B, N, N, C] and its tangent -> bias and tangent [B, N, N, H] (the reference's layout) on
+    the pairs the square-mask attention reads, with the LCA-ALiBi term."""
+    import torch
+
+    from hamiltonzero_amd import _native
+
+    lib = _native.lib()
+    dev = torch.device("cuda:0")
+    B, N, H, n_phys, C, Hd, nb = cfg.B, cfg.N, cfg.H, cfg.n_phys, cfg.d_c, cfg.D, 1
+    d_head = 16
+    rng = np.random.default_rng(cfg.seed)
+
+    def w(*shape):
+        return torch.from_numpy(rng.standard_normal(shape, dtype=np.float32) * np.float32(shape[-2] ** -0.5))
+
+    def small(*shape):
+        return torch.from_numpy(rng.standard_normal(shape, dtype=np.float32) * np.float32(0.1))
+
+    ph = {"w_in": w(C, Hd), "b_in": small(Hd), "norm_w": 1.0 + small(nb, Hd), "w_1": w(nb, Hd, Hd),
+          "b_1": small(nb, Hd), "w_2": w(nb, Hd, Hd), "b_2": small(nb, Hd), "out_norm_w": 1.0 + small(Hd),
+          "w_out": w(Hd, H), "b_out": small(H)}
+    names = ("w_in", "b_in", "norm_w", "w_1", "b_1", "w_2", "b_2", "out_norm_w", "w_out", "b_out")
+    p = {k: v.to(dev) for k, v in ph.items()}
+    edge = torch.randn((B, N, N, C), device=dev, generator=torch.Generator(device=dev).manual_seed(cfg.seed))
+    edge_t = torch.randn((B, N, N, C), device=dev, generator=torch.Generator(device=dev).manual_seed(cfg.seed + 1))
+    maskh = torch.zeros((B, N), dtype=torch.bool)
+    maskh[:, :n_phys] = True
+    mask = maskh.to(torch.uint8).to(dev)
+    slopes_h = 1.5 * torch.exp2(-(torch.arange(H, dtype=torch.float32) * 4.0 / max(H - 1, 1)))
+    slopes = slopes_h.to(dev)
+    e = torch.zeros((B, N, N, H), dtype=torch.float32, device=dev)
+    e_t = torch.zeros_like(e)
+    div = float(np.sqrt(np.float32(d_head)))
+    s = torch.cuda.current_stream(dev).cuda_stream
+
+    def step(i):
+        _native.check(lib.hz_pair_mlp_bias(s, edge.data_ptr(), edge_t.data_ptr(), None, None, mask.data_ptr(),
+                                           *(p[k].data_ptr() for k in names), slopes.data_ptr(), e.data_ptr(),
+                                           e_t.data_ptr(), B, N, N, C, Hd, H, nb, 1, 0, 1.0, 1e-5, div,
+                                           _native.HZ_FLAG_E_QKH))
+
+    ms = timed(step, args.steps, args.warmup, torch.cuda.current_stream(dev))
+    t_s = ms / 1e3
+    pairs = B * n_phys * n_phys
+    flops_pair = 2 * 2 * (C * Hd + 2 * nb * Hd * Hd + Hd * H)  # primal and tangent
+    bytes_pair = 4 * (2 * C + 2 * H)
+    roof = roofline(pairs * bytes_pair, pairs * flops_pair, t_s, "f32")
+    roof.update({"kernel": "pair_mlp_bias_kernel", "traffic": traffic_from_profile(args.config),
+                 "basis": f"computed pairs ({pairs}: the {n_phys} x {n_phys} physical pairs of each walker) x "
+                          f"{flops_pair} flops / {bytes_pair} bytes (edge, edge_t in; e, e_t out)",
+                 "bytes_per_step": pairs * bytes_pair, "flops_per_step": pairs * flops_pair,
+                 "reference_equivalent": {"pairs": B * N * N, "flops_per_step": B * N * N * flops_pair}})
+    cpu = None
+    if not args.no_cpu_baseline:
+        from oracle import cpu_baseline
+
+        n = cfg.cpu_sample
+        eh, eth = edge[:n, :n_phys, :n_phys].cpu().contiguous(), edge_t[:n, :n_phys, :n_phys].cpu().contiguous()
+        r = cpu_baseline.time_mlp_pair_bias_walkers_per_s(eh, eth, ph, 1.0, div, slopes_h, budget_s=args.cpu_budget)
+        got, got_t = e[:n, :n_phys, :n_phys].cpu().numpy(), e_t[:n, :n_phys, :n_phys].cpu().numpy()
+        errs = {"e": rel_err(got, r["e"].numpy()), "e_t": rel_err(got_t, r["e_t"].numpy())}
+        cpu = {"value": r["walkers_per_s"], "unit": "walkers/s", "cores": r["threads"], "kind": "port",
+               "sample": f"the physical {n_phys} x {n_phys} pairs of the first {n} walkers, {r['reps']} reps in "
+                         f"{r['seconds']:.1f} s, torch-CPU fp32 port of the MLP, ALiBi and torch.func.jvp "
+                         f"({r['cpu_model']})",
+               "host_cpus": r["host_cpus"], "check": {"max_rel_err_vs_gpu": errs, "tol": 1e-5,
+                                                      "ok": all(v <= 1e-5 for v in errs.values())}}
+    line = {
+        "metric": cfg.metric, "value": B / t_s, "unit": "walkers/s", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "settle_ms": args.settle_ms, "ms_per_step": ms, "higher_is_better": True,
+        "scaling": "weak", "vs_baseline": None, "dtype": "f32",
+        "data": "synthetic (torch N(0,1) edge and tangent; numpy default_rng weights N(0,1)/sqrt(fan_in))",
+        "config": {"workload": f"{args.config}: {cfg.desc}", "B": B, "N": N, "C": C, "hidden": Hd, "H": H,
+                   "n_blocks": nb, "n_phys": n_phys, "T": 1},
+        "roofline": roof, "cpu_baseline": cpu,
+    }
+    print(json.dumps(line), flush=True)
+    return 0
+
+
 def run_executor(args, cfg):
     """Bench leg of one compiled-executor tree level (hz_quadrilinear_merge, hz_factorized_apply).
     Config fields: B walkers, N node pairs (width), H groups, D rank d_r, n_phys merge_rank."""
@@ -986,6 +1079,8 @@ def main(argv=None):
         return run_rect(args, cfg)
     if cfg.work == "rect_gate":
         return run_rect_gate(args, cfg)
+    if cfg.work == "pair_mlp":
+        return run_pair_mlp(args, cfg)
     if cfg.work == "executor":
         return run_executor(args, cfg)
     if cfg.work == "trunk":

@@ -45,6 +45,7 @@ EXPORTED_SYMBOLS = (
     "hz_compiled_wavefunction_workspace",
     "hz_compiled_wavefunction",
     "hz_pair_bias",
+    "hz_pair_mlp_bias",
 )
 
 
@@ -115,6 +116,10 @@ _SIGNATURES = {
     # stream, edge, edge_t, mask, ln_w, w_in, b_in, w_1, b_1, w_2, b_2, w_out, b_out, e, e_t,
     # B, N, C, hidden, H, T, inner_gain, eps, bias_div, flags
     "hz_pair_bias": ([_P] * 15 + [_I64] * 6 + [_F, _F, _F, _INT], _INT),
+    # stream, edge, edge_t, extra, extra_t, mask, w_in, b_in, norm_w, w_1, b_1, w_2, b_2,
+    # out_norm_w, w_out, b_out, alibi_slopes, e, e_t, B, Nq, Nk, C, hidden, H, n_blocks, T,
+    # row_offset, inner_gain, eps, bias_div, flags
+    "hz_pair_mlp_bias": ([_P] * 19 + [_I64] * 9 + [_F, _F, _F, _INT], _INT),
 }
 
 

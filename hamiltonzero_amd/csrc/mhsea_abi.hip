@@ -394,6 +394,94 @@ int hz_rect_attention_fwd_gated(hipStream_t stream, const float* q, const float*
   return rect_attention(stream, q, k, v, bias, key_mask, y, B, Nq, Nk, H, D, scale, true);
 }
 
+int hz_pair_mlp_bias(hipStream_t stream, const float* edge, const float* edge_t, const float* extra,
+                     const float* extra_t, const uint8_t* mask, const float* w_in, const float* b_in,
+                     const float* norm_w, const float* w_1, const float* b_1, const float* w_2, const float* b_2,
+                     const float* out_norm_w, const float* w_out, const float* b_out, const float* alibi_slopes,
+                     float* e, float* e_t, int64_t B, int64_t Nq, int64_t Nk, int64_t C, int64_t hidden, int64_t H,
+                     int64_t n_blocks, int64_t T, int64_t row_offset, float inner_gain, float eps, float bias_div,
+                     int flags) {
+  if (B < 1 || Nq < 1 || Nk < 1 || Nq > HZ_MAX_N || Nk > HZ_MAX_N)
+    return fail(HZ_EINVAL, "B must be >= 1 and Nq, Nk in [1, %d]", HZ_MAX_N);
+  if (C != 32 && C != 64 && C != 96 && C != 128)
+    return fail(HZ_EINVAL, "C = %lld: edge channels must be 32, 64, 96 or 128", (long long)C);
+  if (hidden != 32 && hidden != 64 && hidden != 128)
+    return fail(HZ_EINVAL, "hidden = %lld: the bias MLP's hidden width must be 32, 64 or 128", (long long)hidden);
+  if (H != 16 && H != 32) return fail(HZ_EINVAL, "H = %lld: heads must be 16 or 32", (long long)H);
+  if (n_blocks < 1 || n_blocks > hz::pair_mlp_max_blocks(static_cast<int>(hidden)))
+    return fail(HZ_EINVAL, "n_blocks = %lld: must be in [1, %d] at hidden width %lld", (long long)n_blocks,
+                hz::pair_mlp_max_blocks(static_cast<int>(hidden)), (long long)hidden);
+  if (T != 0 && T != 1) return fail(HZ_EINVAL, "T = %lld: T must be 0 or 1", (long long)T);
+  if (flags & ~(HZ_FLAG_KEY_MASK | HZ_FLAG_E_QKH)) return fail(HZ_EINVAL, "unknown flag bits 0x%x", flags);
+  if (mask != nullptr && !(flags & HZ_FLAG_KEY_MASK) && Nq != Nk)
+    return fail(HZ_EINVAL, "a square (query and key) mask needs Nq == Nk, got Nq=%lld Nk=%lld; pass HZ_FLAG_KEY_MASK",
+                (long long)Nq, (long long)Nk);
+  if (row_offset < 0 || row_offset + Nq > 0x7fffffffLL) return fail(HZ_EINVAL, "row_offset must be >= 0 and fit int32");
+  if (B * Nq * Nk > (int64_t(1) << 40)) return fail(HZ_EINVAL, "B*Nq*Nk exceeds the supported size");
+  if (!std::isfinite(inner_gain) || !std::isfinite(eps) || eps < 0.0f || !std::isfinite(bias_div) || bias_div == 0.0f)
+    return fail(HZ_EINVAL, "inner_gain and bias_div must be finite (bias_div nonzero), eps finite and >= 0");
+  HZ_REQUIRE(edge);
+  HZ_OPTIONAL(mask);
+  HZ_REQUIRE(w_in);
+  HZ_REQUIRE(b_in);
+  HZ_REQUIRE(norm_w);
+  HZ_REQUIRE(w_1);
+  HZ_REQUIRE(b_1);
+  HZ_REQUIRE(w_2);
+  HZ_REQUIRE(b_2);
+  HZ_REQUIRE(out_norm_w);
+  HZ_REQUIRE(w_out);
+  HZ_REQUIRE(b_out);
+  HZ_OPTIONAL(alibi_slopes);
+  HZ_REQUIRE(e);
+  if (T == 1) {
+    HZ_REQUIRE(edge_t);
+    HZ_REQUIRE(e_t);
+    if (extra != nullptr && extra_t == nullptr) return fail(HZ_ENULL, "extra_t must not be NULL when extra is given and T = 1");
+  }
+  if ((reinterpret_cast<uintptr_t>(extra) | reinterpret_cast<uintptr_t>(extra_t)) & 3u)
+    return fail(HZ_EALIGN, "extra and extra_t must be 4-byte aligned");
+  hz::PairMlpParams p{};
+  p.edge = edge;
+  p.edge_t = T == 1 ? edge_t : nullptr;
+  p.extra = extra;
+  p.extra_t = T == 1 ? extra_t : nullptr;
+  p.mask = mask;
+  p.w_in = w_in;
+  p.b_in = b_in;
+  p.norm_w = norm_w;
+  p.w_1 = w_1;
+  p.b_1 = b_1;
+  p.w_2 = w_2;
+  p.b_2 = b_2;
+  p.out_norm_w = out_norm_w;
+  p.w_out = w_out;
+  p.b_out = b_out;
+  p.slopes = alibi_slopes;
+  p.e = e;
+  p.e_t = T == 1 ? e_t : nullptr;
+  p.B = B;
+  p.Nq = static_cast<int>(Nq);
+  p.Nk = static_cast<int>(Nk);
+  p.n_blocks = static_cast<int>(n_blocks);
+  p.row_offset = static_cast<int>(row_offset);
+  if (flags & HZ_FLAG_E_QKH) {  // [B, Nq, Nk, H]
+    p.e_sq = Nk * H;
+    p.e_sk = H;
+    p.e_sh = 1;
+  } else {  // [B, Nq, H, Nk]
+    p.e_sq = H * Nk;
+    p.e_sh = Nk;
+    p.e_sk = 1;
+  }
+  p.gain = inner_gain;
+  p.eps = eps;
+  p.div = bias_div;
+  p.key_mask = (flags & HZ_FLAG_KEY_MASK) != 0;
+  return launched(hz::launch_pair_mlp_bias(p, static_cast<int>(C), static_cast<int>(hidden), static_cast<int>(H),
+                                           T == 1, stream));
+}
+
 int hz_quadrilinear_merge(hipStream_t stream, const float* T, const float* u_a, const float* u_b, float* out,
                           int64_t M, int64_t G, int64_t R) {
   if (R != 32) return fail(HZ_EINVAL, "the merge rank R must be 32, got %lld", (long long)R);

@@ -193,6 +193,38 @@ struct PairBiasParams {
 };
 hipError_t launch_pair_bias(PairBiasParams p, int C, int H, bool tan, hipStream_t stream);
 
+// The MLP-class pair-bias producer with the LCA-ALiBi term (pair_mlp_bias.hip).
+struct PairMlpParams {
+  const float* edge;        // [B, Nq, Nk, C]
+  const float* edge_t;      // [B, Nq, Nk, C] or null
+  const float* extra;       // [B, Nq, Nk] or null (one more input channel, w_in row C)
+  const float* extra_t;     // [B, Nq, Nk] or null
+  const uint8_t* mask;      // [B, Nk] or null
+  const float* w_in;        // [C (+1), hidden]
+  const float* b_in;        // [hidden]
+  const float* norm_w;      // [n_blocks, hidden]
+  const float* w_1;         // [n_blocks, hidden, hidden]
+  const float* b_1;         // [n_blocks, hidden]
+  const float* w_2;
+  const float* b_2;
+  const float* out_norm_w;  // [hidden]
+  const float* w_out;       // [hidden, H]
+  const float* b_out;       // [H]
+  const float* slopes;      // [H] or null (no LCA-ALiBi term)
+  float* e;
+  float* e_t;
+  int64_t B;
+  int Nq, Nk, n_blocks, row_offset;
+  int64_t e_sq, e_sh, e_sk;
+  float gain, eps, div;
+  bool key_mask;            // compute every query row (key-mask attention semantics)
+  int parts;                // items per walker (set by the launcher)
+  int64_t n_items;          // B * parts (set by the launcher)
+};
+hipError_t launch_pair_mlp_bias(PairMlpParams p, int C, int hidden, int H, bool tan, hipStream_t stream);
+// Blocks whose weights fit the LDS next to the other fragments at this hidden width.
+int pair_mlp_max_blocks(int hidden);
+
 // Rectangular attention with a dense [B, Nq, Nk, H] bias (rect_attention.hip).
 struct RectParams {
   const float* q;      // [B, Nq, H, D]

@@ -53,6 +53,50 @@ int hz_pair_bias(hipStream_t stream, const float* edge, const float* edge_t, con
                  int64_t C, int64_t hidden, int64_t H, int64_t T, float inner_gain, float eps, float bias_div,
                  int flags);
 
+/*
+ * The MLP-class pair-bias producer, with the LCA-ALiBi term. Replaces the coupling-bias
+ * computation of the tree's LevelEdgeAttn (src/hamiltonzero/model/tree.py:1392-1456), of the
+ * readout context's _attend (model/readout_leaf_context.py:694-712) and of the large-N
+ * sequence trunk (evaluation/sequence_trunk.py:962-972, _pair_mlp_tiled + lca_alibi_bias):
+ * bias_mlp is the normalised MLP (model/odd_ops.py:218-276: in_proj, n_blocks residual blocks
+ * each with an RMS norm before its first Linear, an RMS norm before out_proj), per pair
+ *
+ *     h    = x W_in[:C] + xe W_in[C] + b_in          x = edge[b, i, j, :], xe = extra[b, i, j]
+ *     h   += inner_gain * (silu(rms_k(h) W_1[k] + b_1[k]) W_2[k] + b_2[k])   for k < n_blocks
+ *     e    = (rms_out(h) W_out + b_out) / bias_div - slope[h] * lca(row_offset + i, j)
+ *     rms_k(h) = h * norm_w[k] * rsqrt(mean(h^2) + eps)           (_RMS, odd_ops.py:183-215)
+ *     lca(p, q) = min(bit length of p ^ q, 13)    (lca_level, readout_leaf_context.py:140-148)
+ *
+ * and, with T = 1, its forward-mode derivative e_t along (edge_t, extra_t) (parameters fixed;
+ * the ALiBi term is constant). The readout concatenates [edge_n, direction] as the MLP input
+ * (readout_leaf_context.py:694): pass direction as `extra` and W_in with C + 1 rows. The tree
+ * adds the ALiBi term with positions 0..n-1 on both sides (tree.py:1448-1451, only when
+ * level_idx is given: pass alibi_slopes = NULL otherwise); the large-N trunk with the global
+ * row index of its local query rows (sequence_trunk.py:964-971: row_offset).
+ * slopes = lca_fixed_slopes(H) (readout_leaf_context.py:151-154) or any [H] vector.
+ *
+ * Operands (device pointers, float32, 16-byte aligned except extra / extra_t): edge / edge_t
+ * [B, Nq, Nk, C]; extra / extra_t [B, Nq, Nk] or NULL; mask [B, Nk] uint8 or NULL; w_in
+ * [C (+1 with extra), hidden]; b_in [hidden]; norm_w [n_blocks, hidden]; w_1 / w_2
+ * [n_blocks, hidden, hidden]; b_1 / b_2 [n_blocks, hidden]; out_norm_w [hidden]; w_out
+ * [hidden, H]; b_out [H]; alibi_slopes [H] or NULL; e (and e_t) [B, Nq, H, Nk], or
+ * [B, Nq, Nk, H] with HZ_FLAG_E_QKH (the reference's layout; the rectangular attention's).
+ * Sizes: C in {32, 64, 96, 128}; hidden in {32, 64, 128} (level_edge_bias_mlp_dim 128,
+ * readout_context_bias_dim 32, config.py:82,80); H in {16, 32}; n_blocks 1 or 2 (1 at hidden
+ * 128); T in {0, 1}. Mask as hz_pair_bias (keys and, without HZ_FLAG_KEY_MASK, queries; a
+ * square mask needs Nq == Nk): with Nk <= 256 only the pairs the attention reads are written,
+ * beyond that every pair is computed.
+ *
+ * Enqueue-only, nothing allocated, deterministic; 0 or an HZ_E* status with hz_last_error().
+ */
+int hz_pair_mlp_bias(hipStream_t stream, const float* edge, const float* edge_t, const float* extra,
+                     const float* extra_t, const uint8_t* mask, const float* w_in, const float* b_in,
+                     const float* norm_w, const float* w_1, const float* b_1, const float* w_2, const float* b_2,
+                     const float* out_norm_w, const float* w_out, const float* b_out, const float* alibi_slopes,
+                     float* e, float* e_t, int64_t B, int64_t Nq, int64_t Nk, int64_t C, int64_t hidden, int64_t H,
+                     int64_t n_blocks, int64_t T, int64_t row_offset, float inner_gain, float eps, float bias_div,
+                     int flags);
+
 #ifdef __cplusplus
 }
 #endif

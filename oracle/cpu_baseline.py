@@ -200,6 +200,49 @@ def time_rect_queries_per_s(q, k, v, bias, key_mask, scale, budget_s: float = 15
     }
 
 
+def mlp_pair_bias(edge, params, gain, div, slopes=None, eps=1e-5):
+    """The MLP-class coupling bias in torch-CPU float32 (odd_ops.py:256-276 MLP, / sqrt(d),
+    + the LCA-ALiBi term on positions 0..n-1, tree.py:1436-1451): edge [B, N, N, C] ->
+    [B, N, N, H]."""
+    h = edge @ params["w_in"] + params["b_in"]
+    for k in range(params["w_1"].shape[0]):
+        n = h * (params["norm_w"][k] * torch.rsqrt(torch.mean(h * h, dim=-1, keepdim=True) + eps))
+        u = n @ params["w_1"][k] + params["b_1"][k]
+        h = h + gain * ((u * torch.sigmoid(u)) @ params["w_2"][k] + params["b_2"][k])
+    n = h * (params["out_norm_w"] * torch.rsqrt(torch.mean(h * h, dim=-1, keepdim=True) + eps))
+    e = (n @ params["w_out"] + params["b_out"]) / div
+    if slopes is not None:
+        idx = torch.arange(edge.shape[1])
+        x = idx[:, None] ^ idx[None, :]
+        lvl = (x[..., None] >= (2 ** torch.arange(13))).sum(-1).to(e.dtype)
+        e = e - lvl[:, :, None] * slopes
+    return e
+
+
+def time_mlp_pair_bias_walkers_per_s(edge, edge_t, params, gain, div, slopes, budget_s: float = 15.0,
+                                     threads: int | None = None) -> dict:
+    """Time the bias and its forward-mode tangent (torch.func.jvp) on every pair of the
+    walkers of ``edge [B_sample, N, N, C]``; returns walkers/s and (e, e_t) of the last
+    repetition."""
+    threads = threads or default_threads()
+    torch.set_num_threads(threads)
+
+    def fn():
+        return torch.func.jvp(lambda x: mlp_pair_bias(x, params, gain, div, slopes), (edge,), (edge_t,))
+
+    with torch.no_grad():
+        res = fn()
+        reps, t0 = 0, time.perf_counter()
+        while True:
+            res = fn()
+            reps += 1
+            el = time.perf_counter() - t0
+            if el >= budget_s or reps >= 100000:
+                break
+    return {"walkers_per_s": edge.shape[0] * reps / el, "seconds": el, "reps": reps, "threads": threads,
+            "cpu_model": host_cpu_model(), "host_cpus": host_cpus(), "e": res[0], "e_t": res[1]}
+
+
 def rect_block(q, k, v, bias, key_mask, scale, w_o, row_mask):
     """The large-N attention tail in torch-CPU float32 (sequence_trunk.py:973-984): the
     rectangular attention, the head collapse sigmoid(out[:, :, :H/2]) * out[:, :, H/2:] and
