@@ -133,6 +133,12 @@ CONFIGS = {
     "c2vjp": Config("fwd_vjp", 1024, 64, 8, 32, 36, 0, "f32", 1,
                     "forward + VJP (training), fp32, [1024,64,8,32], 36/64 physical sites: forward (out, lse), "
                     "then dq, dk, dv", metric=VJP_METRIC),
+    # The training path with the pair bias every model call passes: its cotangent de is an
+    # output too (the bias comes from the trainable pair MLP).
+    "c2e_vjp": Config("fwd_vjp", 1024, 64, 8, 32, 36, 0, "f32", 1,
+                      "forward + VJP (training) with the pair bias, fp32, [1024,64,8,32], e [1024,64,8,64], "
+                      "36/64 physical sites: forward (out, lse), then dq, dk, dv and de", with_e=True,
+                      metric=VJP_METRIC),
     # The same training path at c3's shape in float32, the precision the reference trains in
     # (pallas_attention.py:16-19 admits float32 only).
     "c3f32": Config("fwd_vjp", 4096, 64, 8, 64, 48, 0, "f32", 2,
@@ -235,7 +241,7 @@ def algorithmic(work, B, N, H, D, n_phys, T, esize, with_e=False):
         n_in, n_out, g_mult, lse_b, n_e = 3 + 4.5, 1 + 3, 6, 2 * N * H * 4, 2
     else:
         raise ValueError(work)
-    n_e_out = 1 if work == "fwd_vjp_gated" else 0
+    n_e_out = 1 if work in ("fwd_vjp", "fwd_vjp_gated") else 0  # de (every pair) when the bias is an input
     e_pad = (n_e + n_e_out) * N * H * N * esize if with_e else 0
     e_eff = (n_e * n_phys * n_phys + n_e_out * N * N) * H * esize if with_e else 0
     padded_bytes = int(B * (N * rowb * (n_in + n_out) + N + lse_b + e_pad))
@@ -394,8 +400,8 @@ def run_attention(args, cfg):
                 d[nm] = torch.empty(shape, dtype=tdt, device=dev)
         if cfg.work == "fwd_vjp_gated":
             d["dout_work"] = torch.empty(shape, dtype=torch.float32, device=dev)
-            if cfg.with_e:
-                d["de"] = torch.empty((B, N, H, N), dtype=tdt, device=dev)
+        if cfg.work in ("fwd_vjp", "fwd_vjp_gated") and cfg.with_e:
+            d["de"] = torch.empty((B, N, H, N), dtype=tdt, device=dev)
         return d
 
     sets = [dev_set() for _ in range(copies)]
@@ -440,7 +446,8 @@ def run_attention(args, cfg):
             lse = P(d, "lse", b0, N * H * 4)
             _native.check(lib.hz_mhsea_fwd(s, q, k, e, v, m, P(d, "out", b0), lse, nb, N, H, D, hz_dtype, 1.0, fl))
             _native.check(lib.hz_mhsea_bwd(s, q, k, e, v, m, lse, P(d, "out", b0), P(d, "dout", b0), P(d, "dq", b0),
-                                           P(d, "dk", b0), None, P(d, "dv", b0), nb, N, H, D, hz_dtype, 1.0, fl))
+                                           P(d, "dk", b0), P(d, "de", b0, erow), P(d, "dv", b0), nb, N, H, D,
+                                           hz_dtype, 1.0, fl))
 
     def step(i):
         d = sets[i % copies]

@@ -13,7 +13,16 @@
 //  Phase B (key-major, wave = 16 keys): S = Q K^T and dP = dout V^T again (cheaper than a
 //    transpose of P and dS through LDS at this size), dv^T += dout^T P, dk^T += Q^T dS.
 // Every result row is written by exactly one wave: deterministic, no atomics.
+//
+// Bias rows (ROWS, float32, e in the [B, N, H, N] layout with N a multiple of 4): the item's
+// physical query rows of e are loaded whole with 16-byte loads one item ahead and staged in
+// LDS (64-float rows, 16-byte chunks XOR-swizzled by row so both phases' gathers are free of
+// bank conflicts), instead of one 4-byte load per score in each phase; de is accumulated in
+// an LDS tile indexed by site (zero-initialised per item, same swizzle) and written as whole
+// rows with 16-byte stores, the zeros of invalid pairs included, instead of one 4-byte store
+// per score and a separate pass of zero stores.
 #include <atomic>
+#include <type_traits>
 
 #include "mhsea_device.h"
 #include "mhsea_launch.h"
@@ -32,6 +41,8 @@ struct BwdStreamShape {
   static constexpr int kItems = KC * C4;
   static constexpr int kPerThread = (kItems + 255) / 256;
   static constexpr size_t kLdsBytes = static_cast<size_t>(4 * kTileFloats + 2 * KC) * 4;
+  // ROWS: the staged e rows and the de tile, 64 x 64 floats each
+  static constexpr size_t kRowsBytes = static_cast<size_t>(2 * KC * KC) * 4;
   // D = 64: one wave per SIMD, so the next item's prefetched rows (80 registers) and the
   // phase-B accumulators fit without scratch (two waves spilled 180-220 bytes per lane and
   // ran 2.4% slower at [4096, 64, 8, 64] fp32). D = 32 keeps three waves with 44-76 bytes of
@@ -58,8 +69,16 @@ __device__ __forceinline__ Sites make_sites(uint32_t mbyte, int N) {
   return st;
 }
 
-template <int D, bool HAS_E, class S>
-__global__ void __launch_bounds__(256, (BwdStreamShape<D>::kWavesPerEu))
+// Float offset of element (row, col) of a 64 x 64 LDS tile whose 16-byte chunks are
+// XOR-swizzled by row: 16 rows read at one column hit 16 different chunks.
+__device__ __forceinline__ int swz64(int row, int col) {
+  return row * 64 + ((((col >> 2) ^ row) & 15) << 2) + (col & 3);
+}
+
+template <int D, bool HAS_E, bool ROWS, class S>
+// ROWS at D = 32 takes 69 KB of LDS, so two workgroups share a CU: two waves per SIMD, whose
+// register budget holds the prefetched e rows without scratch.
+__global__ void __launch_bounds__(256, ((ROWS && D == 32) ? 2 : BwdStreamShape<D>::kWavesPerEu))
     mhsea_bwd_stream_kernel(const BwdParams p) {
   using Sh = BwdStreamShape<D>;
   constexpr int LD = Sh::LD, DG = Sh::DG, DT = Sh::DT, C4 = Sh::C4, NPT = Sh::kPerThread;
@@ -72,6 +91,8 @@ __global__ void __launch_bounds__(256, (BwdStreamShape<D>::kWavesPerEu))
   float* const Gs = Vs + Sh::kTileFloats;               // dout rows
   float* const L2s = Gs + Sh::kTileFloats;              // lse * log2(e) per compacted query
   float* const Dls = L2s + Sh::KC;                      // delta per compacted query
+  float* const Es = Dls + Sh::KC;                       // ROWS: e rows [compacted query][site]
+  float* const Des = Es + Sh::KC * Sh::KC;              // ROWS: de [query site][key site]
 
   const int N = p.N, H = p.H;
   const int64_t nitems = static_cast<int64_t>(p.B) * H;
@@ -95,8 +116,11 @@ __global__ void __launch_bounds__(256, (BwdStreamShape<D>::kWavesPerEu))
 
   Raw4<S> cq[NPT], ck[NPT], cv[NPT], cg[NPT], co[NPT];
   float clse = 0.f;
+  constexpr int NE = ROWS && HAS_E ? 4 : 0;  // e float4 per thread: 64 rows x 16 chunks / 256
+  v4f ce[NE > 0 ? NE : 1];  // ext-vector type: promoted to registers (float4 arrays went to scratch)
+  const int nc4 = N >> 2;                    // 16-byte chunks of one e row (ROWS: N % 4 == 0)
 
-  auto issue_item_loads = [&](int b, int h, const Sites& st) {
+  auto issue_item_loads = [&](int b, int h, const Sites& st) __attribute__((always_inline)) {
     const int qperm = qperm_of(st), kperm = kperm_of(st), nq = nq_of(st), nk = nk_of(st);
 #pragma unroll
     for (int u = 0; u < NPT; ++u) {
@@ -115,6 +139,18 @@ __global__ void __launch_bounds__(256, (BwdStreamShape<D>::kWavesPerEu))
     }
     const int sl = __shfl(qperm, lane, 64);
     clse = p.lse[(static_cast<int64_t>(b) * N + (lane < nq ? sl : 0)) * H + h];
+    if constexpr (NE > 0) {
+      const float* ew = static_cast<const float*>(p.e) + static_cast<int64_t>(b) * N * N * H +
+                        static_cast<int64_t>(h) * p.e_sh;
+#pragma unroll
+      for (int u = 0; u < NE; ++u) {
+        const int it = tid + u * 256;
+        const int r = it >> 4, c4 = it & 15;
+        const int sq = __shfl(qperm, r & 63, 64);
+        const bool ok = r < nq && c4 < nc4;
+        ce[u] = *reinterpret_cast<const v4f*>(ew + static_cast<int64_t>(ok ? sq : 0) * p.e_sq + (ok ? c4 : 0) * 4);
+      }
+    }
   };
   auto load_mask_byte = [&](int b) -> uint32_t {
     return lane < N ? static_cast<uint32_t>(p.mask[static_cast<int64_t>(b) * N + lane]) : 0u;
@@ -157,6 +193,22 @@ __global__ void __launch_bounds__(256, (BwdStreamShape<D>::kWavesPerEu))
       }
     }
     if (tid < 64) L2s[tid] = tid < nq ? clse * kLog2e : INFINITY;
+    if constexpr (ROWS) {
+      // the 64 x 64 tiles: 1024 chunks over 256 threads, chunk u * 256 + tid (written out so
+      // the prefetch registers are never indexed at run time)
+      const int r0 = tid >> 4, c40 = tid & 15;
+      if constexpr (NE > 0) {
+        *reinterpret_cast<v4f*>(Es + swz64(r0, 4 * c40)) = ce[0];
+        *reinterpret_cast<v4f*>(Es + swz64(r0 + 16, 4 * c40)) = ce[1];
+        *reinterpret_cast<v4f*>(Es + swz64(r0 + 32, 4 * c40)) = ce[2];
+        *reinterpret_cast<v4f*>(Es + swz64(r0 + 48, 4 * c40)) = ce[3];
+      }
+      if (p.de != nullptr) {
+#pragma unroll
+        for (int u = 0; u < 4; ++u)
+          *reinterpret_cast<float4*>(Des + swz64(r0 + 16 * u, 4 * c40)) = make_float4(0.f, 0.f, 0.f, 0.f);
+      }
+    }
     const int bc = b, hc = h;
     const Sites sc_ = cur;
     __syncthreads();
@@ -217,13 +269,21 @@ __global__ void __launch_bounds__(256, (BwdStreamShape<D>::kWavesPerEu))
             int ks = 0;
             if constexpr (HAS_E) {
               ks = __shfl(kperm, j & 63, 64);
-              if (valid) sv += load1<S>(p.e, e_row + static_cast<int64_t>(ks) * p.e_sk);
+              if constexpr (ROWS) {
+                if (valid) sv += Es[swz64(jq, ks)];
+              } else {
+                if (valid) sv += load1<S>(p.e, e_row + static_cast<int64_t>(ks) * p.e_sk);
+              }
             }
             const float pv = valid ? lse_weight(sv * kLog2e - lse2) : 0.f;
             dsv[r] = pv * (dp[r] - delta);
             if (p.de != nullptr) {
               if constexpr (!HAS_E) ks = __shfl(kperm, j & 63, 64);
-              if (valid) store1<S>(p.de, e_row + static_cast<int64_t>(ks) * p.e_sk, dsv[r]);
+              if constexpr (ROWS) {
+                if (valid) Des[swz64(qsite, ks)] = dsv[r];
+              } else {
+                if (valid) store1<S>(p.de, e_row + static_cast<int64_t>(ks) * p.e_sk, dsv[r]);
+              }
             }
           }
 #pragma unroll
@@ -285,10 +345,14 @@ __global__ void __launch_bounds__(256, (BwdStreamShape<D>::kWavesPerEu))
             const bool valid = il < nq && kvalid;
             float sv = sc[r];
             if constexpr (HAS_E) {
-              const int qs2 = __shfl(qperm, il & 63, 64);
-              if (valid)
-                sv += load1<S>(p.e, e_walker + static_cast<int64_t>(qs2) * p.e_sq +
-                                        static_cast<int64_t>(ksite) * p.e_sk);
+              if constexpr (ROWS) {
+                if (valid) sv += Es[swz64(il, ksite)];
+              } else {
+                const int qs2 = __shfl(qperm, il & 63, 64);
+                if (valid)
+                  sv += load1<S>(p.e, e_walker + static_cast<int64_t>(qs2) * p.e_sq +
+                                          static_cast<int64_t>(ksite) * p.e_sk);
+              }
             }
             pv[r] = valid ? lse_weight(sv * kLog2e - L2s[il]) : 0.f;
             dsv[r] = pv[r] * (dp[r] - Dls[il]);
@@ -337,7 +401,17 @@ __global__ void __launch_bounds__(256, (BwdStreamShape<D>::kWavesPerEu))
           }
         }
       }
-      if (p.de != nullptr && !key_all) {
+      if constexpr (ROWS) {
+        if (p.de != nullptr) {  // the whole de block of the item from its LDS tile
+          __syncthreads();
+          float* dw = static_cast<float*>(p.de) + e_walker;
+          for (int it = tid; it < N * nc4; it += 256) {
+            const int i = it / nc4, c4 = it - i * nc4;
+            *reinterpret_cast<float4*>(dw + static_cast<int64_t>(i) * p.e_sq + 4 * c4) =
+                *reinterpret_cast<const float4*>(Des + swz64(i, 4 * c4));
+          }
+        }
+      } else if (p.de != nullptr && !key_all) {
         // invalid pairs: every key of a masked query row (square mask), and every masked
         // key of the other rows
         for (int it = tid; it < N * N; it += 256) {
@@ -355,11 +429,11 @@ __global__ void __launch_bounds__(256, (BwdStreamShape<D>::kWavesPerEu))
   }
 }
 
-template <int D, bool HAS_E, class S>
+template <int D, bool HAS_E, bool ROWS, class S>
 hipError_t launch_bwd_stream_t(const BwdParams& p, hipStream_t stream) {
   using Sh = BwdStreamShape<D>;
-  auto kern = mhsea_bwd_stream_kernel<D, HAS_E, S>;
-  const size_t lds = Sh::kLdsBytes;
+  auto kern = mhsea_bwd_stream_kernel<D, HAS_E, ROWS, S>;
+  const size_t lds = Sh::kLdsBytes + (ROWS ? Sh::kRowsBytes : 0);
   if (lds > 64 * 1024) {
     hipError_t err = hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
                                          hipFuncAttributeMaxDynamicSharedMemorySize,
@@ -389,8 +463,16 @@ hipError_t launch_bwd_stream_t(const BwdParams& p, hipStream_t stream) {
 
 template <int D, class S>
 hipError_t dispatch_e(const BwdParams& p, hipStream_t stream) {
-  if (p.e != nullptr) return launch_bwd_stream_t<D, true, S>(p, stream);
-  return launch_bwd_stream_t<D, false, S>(p, stream);
+  // LDS-staged bias rows and de tile: float32, keys contiguous ([B, N, H, N]), N % 4 == 0,
+  // and a bias or a bias cotangent to move
+  if constexpr (std::is_same<S, F32>::value) {
+    if (p.e_sk == 1 && p.N % 4 == 0 && (p.e != nullptr || p.de != nullptr)) {
+      if (p.e != nullptr) return launch_bwd_stream_t<D, true, true, S>(p, stream);
+      return launch_bwd_stream_t<D, false, true, S>(p, stream);
+    }
+  }
+  if (p.e != nullptr) return launch_bwd_stream_t<D, true, false, S>(p, stream);
+  return launch_bwd_stream_t<D, false, false, S>(p, stream);
 }
 
 template <class S>

@@ -59,8 +59,12 @@ def fwd_jvp_gated(q, k, v, mask, qt, kt, vt, e=None, et=None):
 
 
 def fwd_vjp(q, k, v, mask, dout, e=None):
-    """(out, (dq, dk, dv)) by reverse-mode autodiff of :func:`attention`."""
-    out, pullback = torch.func.vjp(lambda a, b, c: attention(a, b, c, mask, e), q, k, v)
+    """(out, (dq, dk, dv[, de])) by reverse-mode autodiff of :func:`attention` (the bias a
+    differentiated input when given)."""
+    if e is None:
+        out, pullback = torch.func.vjp(lambda a, b, c: attention(a, b, c, mask), q, k, v)
+    else:
+        out, pullback = torch.func.vjp(lambda a, b, c, d: attention(a, b, c, mask, d), q, k, v, e)
     return out, pullback(dout)
 
 
@@ -134,8 +138,11 @@ def time_walkers_per_s(work: str, inputs: dict, budget_s: float = 15.0, threads:
             return {"out": attention(q, k, v, mask, e)}
     elif work == "fwd_vjp":
         def fn():
-            out, (dq, dk, dv) = fwd_vjp(q, k, v, mask, inputs["dout"], e)
-            return {"out": out, "dq": dq, "dk": dk, "dv": dv}
+            out, grads = fwd_vjp(q, k, v, mask, inputs["dout"], e)
+            res = {"out": out, "dq": grads[0], "dk": grads[1], "dv": grads[2]}
+            if e is not None:
+                res["de"] = grads[3]
+            return res
     elif work == "fwd_vjp_gated":
         def fn():
             _, grads = fwd_vjp_gated(q, k, v, mask, inputs["dy"], e)
