@@ -1,9 +1,9 @@
 // Producer/consumer forward / forward+tangent / tangent-only MHSEA kernel for float32
 // storage and N <= 64 (every key of a (walker, head) fits one LDS tile).
 //
-// A workgroup is four waves: wave 3 is the producer, waves 0-2 are consumers. A fixed grid
-// of workgroups walks the (walker, head) items; workgroup L takes items L, L+G, L+2G, ...
-// and processes them in "periods", one item per period. In period k
+// A workgroup is four waves: one producer and three consumers (roles by SIMD: pc_role). A
+// fixed grid of workgroups walks the (walker, head) items; workgroup L takes items L, L+G,
+// L+2G, ... and processes them in "periods", one item per period. In period k
 //   - the consumers compute item k from LDS buffer k%2: each owns one 16-query tile of the
 //     compacted query list and runs S^T = K Q^T, the exact softmax (all keys in one tile)
 //     and O^T += V^T P^T on the fp32 matrix cores (v_mfma_f32_16x16x4_f32), with the
@@ -43,6 +43,7 @@ typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
 constexpr int kProducerWave = 3;
 constexpr int kSlots = 4;
 constexpr int kSlotBytes = 144;  // int16 perm[64], int32 n_phys at byte 128
+constexpr int kRoleBytes = 132;  // slot 0: one byte per wave for the role exchange (below)
 constexpr int kDmaBytes = 1024;  // bytes one 16-byte-per-lane wave instruction moves
 
 template <int D, int T>
@@ -185,7 +186,7 @@ struct ItemSeq {
 };
 
 // ------------------------------------------------------------------------------------
-// Producer (wave 3)
+// Producer (role 3)
 // ------------------------------------------------------------------------------------
 template <int D, int T, bool GIVEN_LSE, bool GATED>
 __device__ __forceinline__ void pc_producer(const FwdParams& p, char* lds, const ItemSeq& seq, int cnt) {
@@ -348,7 +349,7 @@ __device__ __forceinline__ void pc_producer(const FwdParams& p, char* lds, const
 }
 
 // ------------------------------------------------------------------------------------
-// Consumers (waves 0-2)
+// Consumers (roles 0-2)
 // ------------------------------------------------------------------------------------
 
 // One consumer's per-item state: where its query rows are, and their fragments (loaded
@@ -850,9 +851,8 @@ __device__ __forceinline__ void pc_tile(const FwdParams& p, const char* buf, con
 }
 
 template <int D, int T, bool GIVEN_LSE, int EM, bool GATED>
-__device__ __forceinline__ void pc_consumer(const FwdParams& p, char* lds, const ItemSeq& seq, int cnt) {
+__device__ __forceinline__ void pc_consumer(const FwdParams& p, char* lds, const ItemSeq& seq, int cnt, int wave) {
   using Sh = PcShape<D, T>;
-  const int wave = threadIdx.x >> 6;
   float* const estage = EM == 2 ? reinterpret_cast<float*>(lds + 2 * Sh::BUF + kSlots * kSlotBytes) +
                                       wave * (1 + T) * (PcEStage<D, T>::kRegion / 4)
                                 : nullptr;
@@ -929,6 +929,33 @@ __device__ __forceinline__ void pc_consumer(const FwdParams& p, char* lds, const
   }
 }
 
+// Roles by SIMD. The hardware spreads a workgroup's four waves over the CU's four SIMDs in an
+// order that differs between the two workgroups sharing the CU (recorded from HW_ID on MI355X:
+// waves 0-3 of one on SIMDs 2, 1, 3, 0, of the other on 1, 3, 0, 2), so roles taken from the
+// wave index put a producer beside a consumer on two SIMDs. Roles here are the ranks of
+// (SIMD, wave index) within the workgroup (a permutation of 0-3 whatever the placement): the
+// wave on the highest SIMD produces, so both workgroups' producers share one SIMD and every
+// consumer shares its SIMD with the other workgroup's consumer of the same query tile. Without
+// a bias, a producer's loads, LDS stores and waits beside a consumer cost that consumer more
+// than a second consumer does (MI355X, same box: c2 91.9 against 95.4 us, the forward of the
+// two-launch route 125.3 against 132.8, the gated c2 shape unchanged). With a bias the
+// consumers stream the bias rows themselves and the wave-index roles are faster (c2e 120.1
+// against 124.1 us, the gated trunk shape 290 against 303), so they keep those. The ranks go
+// through one byte per wave in slot 0 (bytes the site lists never use) before the first
+// barrier.
+__device__ __forceinline__ int pc_role(char* xch) {
+  const int w = threadIdx.x >> 6;
+  constexpr int kHwIdAll = (31 << 11) | 4;  // s_getreg: HW_REG_HW_ID, bits 0-31
+  const int simd = static_cast<int>((__builtin_amdgcn_s_getreg(kHwIdAll) >> 4) & 3);
+  const int key = (simd << 2) | w;
+  if ((threadIdx.x & 63) == 0) xch[w] = static_cast<char>(key);
+  __syncthreads();
+  int role = 0;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) role += xch[i] < key;
+  return __builtin_amdgcn_readfirstlane(role);
+}
+
 template <int D, int T, bool GIVEN_LSE, int EM, bool GATED>
 __global__ void __launch_bounds__(256, 2) mhsea_fwd_pc_kernel(const FwdParams p) {
   using Sh = PcShape<D, T>;
@@ -941,10 +968,11 @@ __global__ void __launch_bounds__(256, 2) mhsea_fwd_pc_kernel(const FwdParams p)
   if (L >= nunits) return;  // workgroup-uniform
   const ItemSeq seq{L, G, nunits, static_cast<uint32_t>(p.H), half};
   const int cnt = static_cast<int>((nunits - L + G - 1) / G) * (GATED ? 2 : 1);
-  if ((threadIdx.x >> 6) == kProducerWave)
+  const int role = EM == 0 ? pc_role(lds + 2 * Sh::BUF + kRoleBytes) : static_cast<int>(threadIdx.x >> 6);
+  if (role == kProducerWave)
     pc_producer<D, T, GIVEN_LSE, GATED>(p, lds, seq, cnt);
   else
-    pc_consumer<D, T, GIVEN_LSE, EM, GATED>(p, lds, seq, cnt);
+    pc_consumer<D, T, GIVEN_LSE, EM, GATED>(p, lds, seq, cnt, role);
   (void)Sh::LDS;
 }
 
