@@ -850,6 +850,194 @@ __device__ __forceinline__ void pc_tile(const FwdParams& p, const char* buf, con
   }
 }
 
+// ---- remainder tile of at most four queries ------------------------------------------
+// An item's last query tile often holds only a few queries (36 sites: 16 + 16 + 4). The
+// 16x16x4 products of pc_tile would spend 12 of their 16 query columns on padding; here
+// v_mfma_f32_4x4x1_16b_f32 (sixteen independent 4x4 outer products per instruction, the same
+// flops per cycle) does the tile's work at a third of the matrix-core time.
+//   S^T: one instruction per feature d; lane l supplies A = K[key l][d] and B = Q[query
+//   l & 3][d] (one ds_bpermute from the lane of the query fragments holding it), so lane
+//   4m + j accumulates the scores of keys 4m .. 4m+3 (registers 0-3) for query j. The softmax
+//   reduces over the 16 lanes of a query (lane bits 2-5).
+//   O^T = V^T P^T, A^T, C^T: block b = 8 part + dg covers features 4dg .. 4dg+3; the keys are
+//   cut into two parts of 4 H4 (H4 = ceil(nk / 8) groups of 4), and in step (m, r) block b
+//   takes key 4 (part H4 + m) + r: lane l supplies A = V[key][l mod 32] and B = P[query
+//   l & 3][key] (one ds_bpermute from the lane holding it in register r). Lane 32 part + 4dg + j
+//   then holds features 4dg .. 4dg+3 of query j for its part; the parts are added across lane
+//   bit 5. Keys nk .. 8 H4 - 1 read rows the producer zero-fills (8 H4 <= the 16-row padded
+//   count) and carry P = 0.
+// Served for D = 32, the plain forward (+ tangents) without bias.
+__device__ __forceinline__ v4f mfma4x4(float a, float b, v4f c) {
+  return __builtin_amdgcn_mfma_f32_4x4x1f32(a, b, c, 0, 0, 0);
+}
+
+// Rotation by n lanes inside each row of 16 lanes (DPP row_ror).
+template <int n>
+__device__ __forceinline__ float row_ror(float x) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), 0x120 + n, 0xF, 0xF, false));
+}
+// Max / sum over the 16 lanes with the same lane & 3.
+__device__ __forceinline__ float query_max(float x) {
+  x = fmaxf(x, row_ror<4>(x));
+  x = fmaxf(x, row_ror<8>(x));
+  return group_max(x);
+}
+__device__ __forceinline__ float query_sum(float x) {
+  x += row_ror<4>(x);
+  x += row_ror<8>(x);
+  return group_sum(x);
+}
+
+template <int D, int T, class PF, class SQ>
+__device__ __forceinline__ void pc_tile_rem4(const FwdParams& p, const char* buf, const QSet<D, T>& qs, int tile,
+                                             PF&& pf, SQ&& sq) {
+  static_assert(D == 32, "four-query remainder tile: D = 32");
+  using Sh = PcShape<D, T>;
+  constexpr int DG = Sh::DG, TT = Sh::TT;
+  const int lane = threadIdx.x & 63;
+  const int j = lane & 3;
+  const int N = p.N, H = p.H;
+  const bool km = p.key_mask != 0;
+  const int b = __builtin_amdgcn_readfirstlane(qs.b), h = __builtin_amdgcn_readfirstlane(qs.h);
+  const int nk = pc_nk(qs.n_phys, km, N);
+  const int nq = pc_nq(qs.n_phys, km, N);
+  const bool qvalid = tile * 16 + j < nq;
+  const int qsite = __shfl(qs.qsite, j, 64);
+  pf();
+
+  const char* K0 = buf;
+  const char* V0 = buf + (T + 1) * Sh::TILE;
+
+  // ---- S^T and dS^T: key row `lane` against the four queries --------------------------
+  float kv[D], ktv[TT][D];
+#pragma unroll
+  for (int c = 0; c < D / 4; ++c) {
+    const int off = swz_off<D>(lane, c);
+    const float4 x = *reinterpret_cast<const float4*>(K0 + off);
+    kv[4 * c] = x.x;
+    kv[4 * c + 1] = x.y;
+    kv[4 * c + 2] = x.z;
+    kv[4 * c + 3] = x.w;
+#pragma unroll
+    for (int t = 0; t < T; ++t) {
+      const float4 y = *reinterpret_cast<const float4*>(K0 + (1 + t) * Sh::TILE + off);
+      ktv[t][4 * c] = y.x;
+      ktv[t][4 * c + 1] = y.y;
+      ktv[t][4 * c + 2] = y.z;
+      ktv[t][4 * c + 3] = y.w;
+    }
+  }
+  v4f sc = zero4();
+  v4f ds[TT];
+#pragma unroll
+  for (int t = 0; t < TT; ++t) ds[t] = zero4();
+#pragma unroll
+  for (int d = 0; d < D; ++d) {
+    const int src = (d / DG) * 16 + j;  // lane (g, c = j) of the fragments holds Q[j][d] at d % DG
+    const float qd = __shfl(qs.qf[d % DG], src, 64);
+    sc = mfma4x4(kv[d], qd, sc);
+#pragma unroll
+    for (int t = 0; t < T; ++t) {
+      const float qtd = __shfl(qs.qtf[t][d % DG], src, 64);
+      ds[t] = mfma4x4(ktv[t][d], qd, ds[t]);
+      ds[t] = mfma4x4(kv[d], qtd, ds[t]);
+    }
+  }
+
+  // ---- scale (log2 e rides on it), validity, exact softmax over the item's keys --------
+  const float qscale = qvalid ? p.scale * kLog2e : 0.f;
+  float mx = -INFINITY;
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    const bool valid = 4 * (lane >> 2) + r < nk;
+    sc[r] = valid ? sc[r] * qscale : -INFINITY;
+#pragma unroll
+    for (int t = 0; t < T; ++t) ds[t][r] = valid ? ds[t][r] * qscale : 0.f;
+    mx = fmaxf(mx, sc[r]);
+  }
+  mx = query_max(mx);
+  float lsum = 0.f;
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    sc[r] = fast_exp2(sc[r] - mx);
+    lsum += sc[r];
+  }
+  float mu[TT];
+#pragma unroll
+  for (int t = 0; t < T; ++t) {
+    ds[t] *= sc;
+    mu[t] = (ds[t][0] + ds[t][1]) + (ds[t][2] + ds[t][3]);
+  }
+
+  // ---- O^T, A^T, C^T ---------------------------------------------------------------------
+  const int part = lane >> 5;
+  const int h4 = (nk + 7) >> 3;
+  const int dcol = lane & 31;
+  v4f o = zero4();
+  v4f at[TT], ct[TT];
+#pragma unroll
+  for (int t = 0; t < TT; ++t) at[t] = ct[t] = zero4();
+  for (int m = 0; m < h4; ++m) {
+    const int grp = part * h4 + m;
+    const int src = 4 * grp + j;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int off = swz_off<D>(4 * grp + r, dcol >> 2) + (dcol & 3) * 4;
+      const float vv = *reinterpret_cast<const float*>(V0 + off);
+      const float pv = __shfl(sc[r], src, 64);
+      o = mfma4x4(vv, pv, o);
+#pragma unroll
+      for (int t = 0; t < T; ++t) {
+        const float pd = __shfl(ds[t][r], src, 64);
+        const float vt = *reinterpret_cast<const float*>(V0 + (1 + t) * Sh::TILE + off);
+        at[t] = mfma4x4(vv, pd, at[t]);
+        ct[t] = mfma4x4(vt, pv, ct[t]);
+      }
+    }
+  }
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    o[r] = xor32_pair_sum(o[r]);
+#pragma unroll
+    for (int t = 0; t < T; ++t) {
+      at[t][r] = xor32_pair_sum(at[t][r]);
+      ct[t][r] = xor32_pair_sum(ct[t][r]);
+    }
+  }
+
+  const float ltot = query_sum(lsum);
+  const float inv = __builtin_amdgcn_rcpf(ltot);  // ltot >= 1: the maximum key contributes 2^0
+  const float inv_ln2 = inv * kLn2;
+  float mut[TT];
+#pragma unroll
+  for (int t = 0; t < T; ++t) mut[t] = query_sum(mu[t]) * inv_ln2;
+  float ov[4];
+#pragma unroll
+  for (int r = 0; r < 4; ++r) ov[r] = o[r] * inv;
+  sq();
+
+  // ---- stores: lanes 0-31 (part 0) write features 4 dg .. 4 dg + 3 of query j ------------
+  const int64_t wrow = static_cast<int64_t>(N) * H * D;
+  const int obytes = static_cast<int>(wrow * 4);
+  const int obase = (qsite * H + h) * D;
+  const int voff = (qvalid && part == 0) ? (obase + 4 * (lane >> 2)) * 4 : obytes;
+  const __amdgpu_buffer_rsrc_t o_rs = make_rsrc(static_cast<float*>(p.out) + b * wrow, obytes);
+  buf_store4(o_rs, voff, ov[0], ov[1], ov[2], ov[3]);
+  const int lbytes = N * H * 4;
+  const __amdgpu_buffer_rsrc_t l_rs =
+      make_rsrc(p.lse != nullptr ? p.lse + static_cast<int64_t>(b) * N * H : nullptr, p.lse != nullptr ? lbytes : 0);
+  const int lvoff = (qvalid && lane < 4) ? (qsite * H + h) * 4 : lbytes;
+  __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint((mx + log2f(ltot)) * kLn2), l_rs, lvoff, 0, 0);
+#pragma unroll
+  for (int t = 0; t < T; ++t) {
+    const __amdgpu_buffer_rsrc_t t_rs = make_rsrc(static_cast<float*>(p.tout) + t * p.t_stride + b * wrow, obytes);
+    float tv[4];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) tv[r] = fmaf(-mut[t], ov[r], fmaf(at[t][r], inv_ln2, ct[t][r] * inv));
+    buf_store4(t_rs, voff, tv[0], tv[1], tv[2], tv[3]);
+  }
+}
+
 template <int D, int T, bool GIVEN_LSE, int EM, bool GATED>
 __device__ __forceinline__ void pc_consumer(const FwdParams& p, char* lds, const ItemSeq& seq, int cnt, int wave) {
   using Sh = PcShape<D, T>;
@@ -886,7 +1074,11 @@ __device__ __forceinline__ void pc_consumer(const FwdParams& p, char* lds, const
     auto pf = [&]() { prefetch(nx, qs, k + 1); };
     auto sq = [&]() { settle_q<D, T, GIVEN_LSE>(nx); };
     const int16_t* sp = slot_perm(k);
-    if (wave * 16 < nq) {
+    // Remainder tiles of at most four queries take the 4x4-block path where it is built.
+    constexpr bool kRem4 = D == 32 && !GIVEN_LSE && EM == 0 && R == 0;
+    if (kRem4 && wave * 16 < nq && nq - wave * 16 <= 4) {
+      if constexpr (kRem4) pc_tile_rem4<D, T>(p, buf, qs, wave, pf, sq);
+    } else if (wave * 16 < nq) {
       switch ((nk + 15) >> 4) {
         case 1: pc_tile<D, T, GIVEN_LSE, EM, 1, R>(p, buf, sp, qs, wave, pf, sq, gm, estage); break;
         case 2: pc_tile<D, T, GIVEN_LSE, EM, 2, R>(p, buf, sp, qs, wave, pf, sq, gm, estage); break;
@@ -902,11 +1094,15 @@ __device__ __forceinline__ void pc_consumer(const FwdParams& p, char* lds, const
     if (wave == 0 && 3 * 16 < nq) {
       QSet<D, T> q3;
       pc_load_q<D, T, GIVEN_LSE>(p, q3, qs.b, qs.h, qs.n_phys, sp, 3);
-      switch ((nk + 15) >> 4) {
-        case 1: pc_tile<D, T, GIVEN_LSE, EM, 1, R>(p, buf, sp, q3, 3, [] {}, [] {}, gx, estage); break;
-        case 2: pc_tile<D, T, GIVEN_LSE, EM, 2, R>(p, buf, sp, q3, 3, [] {}, [] {}, gx, estage); break;
-        case 3: pc_tile<D, T, GIVEN_LSE, EM, 3, R>(p, buf, sp, q3, 3, [] {}, [] {}, gx, estage); break;
-        default: pc_tile<D, T, GIVEN_LSE, EM, 4, R>(p, buf, sp, q3, 3, [] {}, [] {}, gx, estage); break;
+      if (kRem4 && nq - 3 * 16 <= 4) {
+        if constexpr (kRem4) pc_tile_rem4<D, T>(p, buf, q3, 3, [] {}, [] {});
+      } else {
+        switch ((nk + 15) >> 4) {
+          case 1: pc_tile<D, T, GIVEN_LSE, EM, 1, R>(p, buf, sp, q3, 3, [] {}, [] {}, gx, estage); break;
+          case 2: pc_tile<D, T, GIVEN_LSE, EM, 2, R>(p, buf, sp, q3, 3, [] {}, [] {}, gx, estage); break;
+          case 3: pc_tile<D, T, GIVEN_LSE, EM, 3, R>(p, buf, sp, q3, 3, [] {}, [] {}, gx, estage); break;
+          default: pc_tile<D, T, GIVEN_LSE, EM, 4, R>(p, buf, sp, q3, 3, [] {}, [] {}, gx, estage); break;
+        }
       }
     }
     __builtin_amdgcn_s_waitcnt(kWaitLgkm0);

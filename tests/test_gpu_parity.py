@@ -111,6 +111,16 @@ CASES = [
     ("n44_d8_t2_rows_bias", 3, 44, 2, 8, 30, True, True, "qhk", False, 0.5, 2, False),
     ("n60_d16_keymask_rows_bias", 3, 60, 2, 16, 20, True, True, "qhk", True, 1.0, 1, False),
     ("n37_d16_unaligned_rows_bias", 3, 37, 2, 16, 25, True, True, "qhk", False, 1.0, 1, False),
+    # D = 32 without bias: last query tiles of at most four queries (the 4x4-block remainder
+    # path) as tile 0, 1, 2 and, through the fourth tile of n > 48, 3; the key mask with and
+    # without physical sites; T = 2; walkers whose site counts differ
+    ("n64_d32_rem4_sites1", 4, 64, 2, 32, 1, True, False, "qhk", False, 1.0, 1, False),
+    ("n64_d32_rem4_sites20_t2", 4, 64, 2, 32, 20, True, False, "qhk", False, 0.5, 2, False),
+    ("n64_d32_rem4_sites34", 4, 64, 3, 32, 34, True, False, "qhk", False, 1.0, 1, False),
+    ("n64_d32_rem4_sites50", 3, 64, 2, 32, 50, True, False, "qhk", False, 1.0, 1, False),
+    ("n36_d32_keymask_rem4", 3, 36, 2, 32, 20, True, False, "qhk", True, 1.0, 1, False),
+    ("n35_d32_keymask_none_rem4", 2, 35, 2, 32, 0, False, False, "qhk", True, 1.0, 2, False),
+    ("n64_d32_mixed_counts_nobias", 24, 64, 3, 32, -1, True, False, "qhk", False, 1.0, 1, False),
     # float32 D = 64, N <= 64: one tangent (streaming kernel) and two (LDS-streaming kernel)
     ("n64_d64_t1_fp32", 3, 64, 2, 64, 48, False, False, "qhk", False, 1.0, 1, False),
     ("n64_d64_t2_fp32_bias", 3, 64, 2, 64, 48, True, True, "qkh", False, 0.5, 2, False),
