@@ -61,10 +61,12 @@ class Config:
 
     work: fwd | fwd_jvp | fwd_jvp_split | fwd_jvp_gated | fwd_vjp | rect. chunk: walkers
     per launch (the step walks the batch in chunks). with_e: pair bias e [B,N,H,N] (and its
-    tangents) present. cpu_sample: walkers of the CPU baseline's sample."""
+    tangents) present; e_layout "compact": handed to the kernels in the compacted physical-pair
+    layout (HZ_FLAG_E_COMPACT, as hz_pair_bias writes it for the trunk). cpu_sample: walkers of
+    the CPU baseline's sample."""
 
     def __init__(self, work, B, N, H, D, n_phys, T, dtype, seed, desc, *, chunk=None, with_e=False,
-                 cpu_sample=64, metric=METRIC, d_c=0):
+                 cpu_sample=64, metric=METRIC, d_c=0, e_layout="qhk"):
         self.work, self.B, self.N, self.H, self.D = work, B, N, H, D
         self.n_phys, self.T, self.dtype, self.seed, self.desc = n_phys, T, dtype, seed, desc
         self.chunk = chunk or B
@@ -72,6 +74,7 @@ class Config:
         self.cpu_sample = cpu_sample
         self.metric = metric
         self.d_c = d_c
+        self.e_layout = e_layout
 
 
 CONFIGS = {
@@ -103,9 +106,10 @@ CONFIGS = {
     # The trunk's own attention call (config.py:20,26: 16 heads of 16 dims, doubled for the
     # gate) with its pair bias, through the fused collapse.
     "gate_trunk": Config("fwd_jvp_gated", 1024, 64, 32, 16, 36, 1, "f32", 1,
-                         "the trunk's attention call: [1024,64,32,16] with pair bias e [1024,64,32,64] and its "
-                         "tangent, gate collapse fused -> y, ydot [1024,64,16,16], 36/64 physical sites",
-                         with_e=True, metric=GATE_METRIC),
+                         "the trunk's attention call: [1024,64,32,16] with pair bias e and its tangent in the "
+                         "compacted physical-pair layout (as hz_pair_bias writes it), gate collapse fused -> y, "
+                         "ydot [1024,64,16,16], 36/64 physical sites",
+                         with_e=True, metric=GATE_METRIC, e_layout="compact"),
     # One tree level of the compiled per-walker executor at the fine-tune ranks: the
     # quadrilinear merge of node pairs and the residual factorized apply
     # (compiled/execute.py:103-104; merge_dim 1536 = 48 groups of rank 32, merge_rank 1024).
@@ -360,7 +364,7 @@ def draw_inputs(cfg):
 def run_attention(args, cfg):
     import torch
 
-    from hamiltonzero_amd import _native
+    from hamiltonzero_amd import _native, kernels
 
     lib = _native.lib()
     tdt = torch.bfloat16 if cfg.dtype == "bf16" else torch.float32
@@ -380,6 +384,8 @@ def run_attention(args, cfg):
     if args.buffer_sets:
         copies = args.buffer_sets
 
+    compact = cfg.with_e and cfg.e_layout == "compact"
+
     def dev_set():
         d = {}
         for nm, x in host.items():
@@ -387,6 +393,11 @@ def run_attention(args, cfg):
                 d[nm] = torch.from_numpy(x.astype(np.uint8)).to(dev)
             else:
                 d[nm] = torch.from_numpy(x).to(device=dev, dtype=tdt).contiguous()
+        if compact:  # the layout conversion happens once, outside the timed steps
+            m = d["mask"]
+            d["e"] = kernels.compact_bias(d["e"], m)
+            if "et" in d:
+                d["et"] = torch.stack([kernels.compact_bias(x, m) for x in d["et"]])
         d["out"] = torch.empty(shape, dtype=tdt, device=dev)
         d["lse"] = torch.empty((B, N, H), dtype=torch.float32, device=dev)
         if cfg.work in ("fwd_jvp", "fwd_jvp_split"):
@@ -408,8 +419,9 @@ def run_attention(args, cfg):
     stream = torch.cuda.current_stream(dev)
     s = stream.cuda_stream
     fl = _native.HZ_FLAG_GENERIC if args.generic else 0
+    fl_e = _native.HZ_FLAG_E_COMPACT if compact else 0
     row = N * H * D * esize  # bytes of one walker of a [B,N,H,D] tensor
-    erow = N * H * N * esize  # bytes of one walker of e
+    erow = int(np.prod(kernels.e_shape(1, N, H, cfg.e_layout if cfg.with_e else "qhk"))) * esize  # one walker of e
 
     def P(d, nm, b0=0, per=row):
         t = d.get(nm)
@@ -435,7 +447,7 @@ def run_attention(args, cfg):
         elif cfg.work == "fwd_jvp_gated":
             _native.check(lib.hz_mhsea_fwd_jvp_gated(s, q, k, e, v, m, P(d, "qt", b0), P(d, "kt", b0), et,
                                                      P(d, "vt", b0), T, P(d, "y", b0, row // 2),
-                                                     P(d, "ty", b0, row // 2), nb, N, H, D, 1.0, 0))
+                                                     P(d, "ty", b0, row // 2), nb, N, H, D, 1.0, fl | fl_e))
         elif cfg.work == "fwd_vjp_gated":
             lse = P(d, "lse", b0, N * H * 4)
             _native.check(lib.hz_mhsea_fwd(s, q, k, e, v, m, P(d, "out", b0), lse, nb, N, H, D, hz_dtype, 1.0, fl))
@@ -853,14 +865,15 @@ def run_executor(args, cfg):
 
 def run_trunk(args, cfg):
     """Bench leg of the trunk attention with its produced bias: hz_pair_bias (edge, edge_t ->
-    e, e_t in the attention layout), hz_mhsea_fwd_jvp_gated, then W_O (hz_gated_out_proj).
+    e, e_t in the compacted physical-pair layout), hz_mhsea_fwd_jvp_gated, then W_O
+    (hz_gated_out_proj).
     Config: B, N, H (kernel heads), D (d_head), n_phys, T = 1; edge channels 96, bias hidden
     64. W_O receives the site mask: the gated attention writes the masked sites' rows of y as
     exact zeros and W_O has no bias (trunk.py:54), so the masked product, which skips those
     rows, equals the reference's unmasked W_O."""
     import torch
 
-    from hamiltonzero_amd import _native
+    from hamiltonzero_amd import _native, kernels
 
     lib = _native.lib()
     dev = torch.device("cuda:0")
@@ -884,8 +897,10 @@ def run_trunk(args, cfg):
               "b_2": rnd((HID,), 0.1), "w_out": rnd((HID, H), HID ** -0.5), "b_out": rnd((H,), 0.1)}
     mask = torch.zeros((B, N), dtype=torch.uint8, device=dev)
     mask[:, :n_phys] = 1
-    d["e"] = torch.zeros((B, N, H, N), dtype=torch.float32, device=dev)
-    d["et"] = torch.zeros((1, B, N, H, N), dtype=torch.float32, device=dev)
+    eshape = kernels.e_shape(B, N, H, "compact")  # the layout the N <= 64 kernel reads cheapest
+    d["e"] = torch.zeros(eshape, dtype=torch.float32, device=dev)
+    d["et"] = torch.zeros((1, *eshape), dtype=torch.float32, device=dev)
+    fl_e = _native.HZ_FLAG_E_COMPACT
     d["y"] = torch.empty((B, N, H // 2, D), dtype=torch.float32, device=dev)
     d["ty"] = torch.empty((1, B, N, H // 2, D), dtype=torch.float32, device=dev)
     stream = torch.cuda.current_stream(dev)
@@ -896,12 +911,12 @@ def run_trunk(args, cfg):
 
     def produce(i):
         _native.check(lib.hz_pair_bias(s, P(d["edge"]), P(d["edge_t"]), P(mask), *(P(params[n]) for n in names),
-                                       P(d["e"]), P(d["et"]), B, N, C, HID, H, 1, gain, 1e-5, div, 0))
+                                       P(d["e"]), P(d["et"]), B, N, C, HID, H, 1, gain, 1e-5, div, fl_e))
 
     def attend(i):
         _native.check(lib.hz_mhsea_fwd_jvp_gated(s, P(d["q"]), P(d["k"]), P(d["e"]), P(d["v"]), P(mask), P(d["qt"]),
                                                  P(d["kt"]), P(d["et"]), P(d["vt"]), 1, P(d["y"]), P(d["ty"]), B, N,
-                                                 H, D, 1.0, 0))
+                                                 H, D, 1.0, fl_e))
 
     def project(i):
         _native.check(lib.hz_gated_out_proj(s, P(d["y"]), P(d["ty"]), P(w_o), P(mask), P(d["delta"]),

@@ -18,6 +18,7 @@ HZ_DTYPE_BF16 = 1
 HZ_FLAG_KEY_MASK = 1
 HZ_FLAG_E_QKH = 2
 HZ_FLAG_GENERIC = 4
+HZ_FLAG_E_COMPACT = 8
 HZ_MAX_N = 16384
 
 HZ_OK = 0

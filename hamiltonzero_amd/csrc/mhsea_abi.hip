@@ -31,7 +31,7 @@ bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) ==
 
 // Shared validation of the dimensions and flags (mirrors the shape assertions of
 // _validate_primals, mhsea_tuned.py:29-50, and the head-dim set of pallas_attention.py:13).
-int check_dims(int64_t B, int64_t N, int64_t H, int64_t D, int dtype, int flags) {
+int check_dims(int64_t B, int64_t N, int64_t H, int64_t D, int dtype, int flags, bool compact_ok = false) {
   if (B < 1 || H < 1) return fail(HZ_EINVAL, "B and H must be >= 1, got B=%lld H=%lld", (long long)B, (long long)H);
   if (N < 1 || N > HZ_MAX_N)
     return fail(HZ_EINVAL, "N must be in [1, %d], got %lld", HZ_MAX_N, (long long)N);
@@ -39,13 +39,30 @@ int check_dims(int64_t B, int64_t N, int64_t H, int64_t D, int dtype, int flags)
     return fail(HZ_EINVAL, "head dimension must be one of [8, 16, 32, 64], got %lld", (long long)D);
   if (dtype != HZ_DTYPE_F32 && dtype != HZ_DTYPE_BF16)
     return fail(HZ_EINVAL, "dtype must be HZ_DTYPE_F32 (0) or HZ_DTYPE_BF16 (1), got %d", dtype);
-  if (flags & ~(HZ_FLAG_KEY_MASK | HZ_FLAG_E_QKH | HZ_FLAG_GENERIC)) return fail(HZ_EINVAL, "unknown flag bits 0x%x", flags);
+  if (flags & ~(HZ_FLAG_KEY_MASK | HZ_FLAG_E_QKH | HZ_FLAG_GENERIC | HZ_FLAG_E_COMPACT))
+    return fail(HZ_EINVAL, "unknown flag bits 0x%x", flags);
+  if ((flags & HZ_FLAG_E_COMPACT) && !compact_ok)
+    return fail(HZ_EINVAL, "HZ_FLAG_E_COMPACT is read by the forward family only (fwd, jvp, fwd_jvp, fwd_jvp_gated)");
   const int64_t nwg = B * H * ((N + 63) / 64);
   if (nwg > 0x7fffffffLL) return fail(HZ_EINVAL, "B*H*ceil(N/64) = %lld exceeds the grid limit", (long long)nwg);
   if (B * N > 0x7fffffffLL)
     return fail(HZ_EINVAL, "B*N = %lld exceeds the supported mask size", (long long)(B * N));
   if (B * N * H * N > (int64_t(1) << 46))
     return fail(HZ_EINVAL, "B*N*H*N = %lld exceeds the supported tensor size", (long long)(B * N * H * N));
+  return HZ_OK;
+}
+
+// The compacted bias layout is read by the N <= 64 producer/consumer kernel only: square
+// mask, float32, the kernel's shapes (with tangents, in passes of one direction where two
+// do not fit it).
+int check_compact(int64_t N, int64_t H, int64_t D, int dtype, int flags, int64_t T) {
+  if (!(flags & HZ_FLAG_E_COMPACT)) return HZ_OK;
+  if (flags & (HZ_FLAG_KEY_MASK | HZ_FLAG_E_QKH | HZ_FLAG_GENERIC))
+    return fail(HZ_EINVAL, "HZ_FLAG_E_COMPACT excludes HZ_FLAG_KEY_MASK, HZ_FLAG_E_QKH and HZ_FLAG_GENERIC");
+  const int t = T > 0 ? 1 : 0;
+  if (dtype != HZ_DTYPE_F32 || !hz::pc_fwd_supported(static_cast<int>(N), static_cast<int>(H), static_cast<int>(D), t, dtype))
+    return fail(HZ_EINVAL, "HZ_FLAG_E_COMPACT needs float32, N <= 64 and D in [8, 16, 32] (N=%lld, D=%lld)",
+                (long long)N, (long long)D);
   return HZ_OK;
 }
 
@@ -95,6 +112,10 @@ hz::FwdParams fwd_params(const void* q, const void* k, const void* e, const void
   p.t_stride = B * N * H * D;
   p.et_stride = B * N * H * N;
   set_e_strides(N, H, flags, p.e_sq, p.e_sh, p.e_sk);
+  if (flags & HZ_FLAG_E_COMPACT) {
+    p.e_compact = 1;
+    p.et_stride = B * H * N * ((N + 3) & ~int64_t(3));
+  }
   p.scale = scale;
   p.key_mask = (flags & HZ_FLAG_KEY_MASK) ? 1 : 0;
   p.masked_lse = -10000.0f + std::log(static_cast<float>(N));
@@ -112,8 +133,10 @@ int run_tangent_groups(hz::FwdParams p, int64_t D, int64_t T, bool given_lse, in
   const int64_t ts = p.t_stride, es = p.et_stride;
   void* const out0 = p.out;
   float* const lse0 = p.lse;
-  for (int64_t t0 = 0; t0 < T; t0 += 2) {
-    const int tn = static_cast<int>(T - t0 < 2 ? T - t0 : 2);
+  // groups of two directions; one where the compacted bias layout's kernel takes only one
+  const int64_t tg = (p.e_compact && !hz::pc_fwd_supported(p.N, p.H, static_cast<int>(D), 2, dtype)) ? 1 : 2;
+  for (int64_t t0 = 0; t0 < T; t0 += tg) {
+    const int tn = static_cast<int>(T - t0 < tg ? T - t0 : tg);
     auto shift = [&](const void* base, int64_t stride) -> const void* {
       return base == nullptr ? nullptr : static_cast<const char*>(base) + t0 * stride * eb;
     };
@@ -203,7 +226,8 @@ const char* hz_last_error(void) { return g_err; }
 int hz_mhsea_fwd(hipStream_t stream, const void* q, const void* k, const void* e,
                  const void* v, const uint8_t* mask, void* out, float* lse, int64_t B,
                  int64_t N, int64_t H, int64_t D, int dtype, float scale, int flags) {
-  if (int rc = check_dims(B, N, H, D, dtype, flags)) return rc;
+  if (int rc = check_dims(B, N, H, D, dtype, flags, true)) return rc;
+  if (int rc = check_compact(N, H, D, dtype, flags, 0)) return rc;
   HZ_REQUIRE(q);
   HZ_REQUIRE(k);
   HZ_REQUIRE(v);
@@ -224,8 +248,9 @@ int hz_mhsea_jvp(hipStream_t stream, const void* q, const void* k, const void* e
                  const void* qt, const void* kt, const void* et, const void* vt, int64_t T,
                  void* tout, int64_t B, int64_t N, int64_t H, int64_t D, int dtype,
                  float scale, int flags) {
-  if (int rc = check_dims(B, N, H, D, dtype, flags)) return rc;
+  if (int rc = check_dims(B, N, H, D, dtype, flags, true)) return rc;
   if (T < 1 || T > 4096) return fail(HZ_EINVAL, "T must be in [1, 4096], got %lld", (long long)T);
+  if (int rc = check_compact(N, H, D, dtype, flags, T)) return rc;
   HZ_REQUIRE(q);
   HZ_REQUIRE(k);
   HZ_REQUIRE(v);
@@ -252,8 +277,9 @@ int hz_mhsea_fwd_jvp(hipStream_t stream, const void* q, const void* k, const voi
                      const void* et, const void* vt, int64_t T, void* out, float* lse,
                      void* tout, int64_t B, int64_t N, int64_t H, int64_t D, int dtype,
                      float scale, int flags) {
-  if (int rc = check_dims(B, N, H, D, dtype, flags)) return rc;
+  if (int rc = check_dims(B, N, H, D, dtype, flags, true)) return rc;
   if (T < 1 || T > 4096) return fail(HZ_EINVAL, "T must be in [1, 4096], got %lld", (long long)T);
+  if (int rc = check_compact(N, H, D, dtype, flags, T)) return rc;
   HZ_REQUIRE(q);
   HZ_REQUIRE(k);
   HZ_REQUIRE(v);
@@ -279,8 +305,9 @@ int hz_mhsea_fwd_jvp_gated(hipStream_t stream, const void* q, const void* k, con
                            const void* v, const uint8_t* mask, const void* qt, const void* kt,
                            const void* et, const void* vt, int64_t T, void* y, void* ty,
                            int64_t B, int64_t N, int64_t H, int64_t D, float scale, int flags) {
-  if (int rc = check_dims(B, N, H, D, HZ_DTYPE_F32, flags)) return rc;
+  if (int rc = check_dims(B, N, H, D, HZ_DTYPE_F32, flags, true)) return rc;
   if (T < 0 || T > 2) return fail(HZ_EINVAL, "T must be in [0, 2] for the gated collapse, got %lld", (long long)T);
+  if (int rc = check_compact(N, H, D, HZ_DTYPE_F32, flags, T)) return rc;
   if (H % 2 != 0) return fail(HZ_EINVAL, "the gated collapse pairs head h with h + H/2: H must be even, got %lld", (long long)H);
   // The producer/consumer kernel where it serves the shape (fp32, N <= 64, D <= 32), in
   // passes of its tangent variants; otherwise (and with HZ_FLAG_GENERIC) the LDS-streaming
@@ -549,7 +576,11 @@ int hz_pair_bias(hipStream_t stream, const float* edge, const float* edge_t, con
   if (hidden != 64) return fail(HZ_EINVAL, "hidden = %lld: the bias MLP's hidden width must be 64", (long long)hidden);
   if (H != 16 && H != 32 && H != 64) return fail(HZ_EINVAL, "H = %lld: heads must be 16, 32 or 64", (long long)H);
   if (T != 0 && T != 1) return fail(HZ_EINVAL, "T = %lld: T must be 0 or 1", (long long)T);
-  if (flags & ~(HZ_FLAG_KEY_MASK | HZ_FLAG_E_QKH)) return fail(HZ_EINVAL, "unknown flag bits 0x%x", flags);
+  if (flags & ~(HZ_FLAG_KEY_MASK | HZ_FLAG_E_QKH | HZ_FLAG_E_COMPACT)) return fail(HZ_EINVAL, "unknown flag bits 0x%x", flags);
+  if ((flags & HZ_FLAG_E_COMPACT) && (flags & (HZ_FLAG_KEY_MASK | HZ_FLAG_E_QKH)))
+    return fail(HZ_EINVAL, "HZ_FLAG_E_COMPACT excludes HZ_FLAG_KEY_MASK and HZ_FLAG_E_QKH");
+  if ((flags & HZ_FLAG_E_COMPACT) && mask != nullptr && N > 256)
+    return fail(HZ_EINVAL, "HZ_FLAG_E_COMPACT with a mask needs N <= 256, got %lld", (long long)N);
   if (!std::isfinite(inner_gain) || !std::isfinite(eps) || eps < 0.0f || !std::isfinite(bias_div) || bias_div == 0.0f)
     return fail(HZ_EINVAL, "inner_gain and bias_div must be finite (bias_div nonzero), eps finite and >= 0");
   HZ_REQUIRE(edge);
@@ -586,6 +617,7 @@ int hz_pair_bias(hipStream_t stream, const float* edge, const float* edge_t, con
   p.B = B;
   p.N = static_cast<int>(N);
   set_e_strides(N, H, flags, p.e_sq, p.e_sh, p.e_sk);
+  if (flags & HZ_FLAG_E_COMPACT) p.e_blk = N * ((N + 3) & ~int64_t(3));
   p.gain = inner_gain;
   p.eps = eps;
   p.div = bias_div;

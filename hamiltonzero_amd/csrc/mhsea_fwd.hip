@@ -577,6 +577,8 @@ hipError_t launch_fwd_gated_generic(const FwdParams& p, int D, int T, hipStream_
 
 hipError_t launch_fwd(const FwdParams& p, int D, int T, bool given_lse, int dtype,
                       hipStream_t stream) {
+  if (p.e_compact)  // the compacted bias layout is read by the producer/consumer kernel only
+    return pc_fwd_supported(p.N, p.H, D, T, dtype) ? launch_fwd_pc(p, D, T, given_lse, stream) : hipErrorInvalidValue;
   if (!p.force_generic) {
     if (dtype == 1 && bf16_ws_fwd_supported(p, D, given_lse)) return launch_fwd_bf16_ws(p, T, stream);
     if (dtype == 1 && bf16_large_fwd_supported(p.N, D)) return launch_fwd_bf16_large(p, D, T, given_lse, stream);

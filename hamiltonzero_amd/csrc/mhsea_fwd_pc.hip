@@ -498,8 +498,13 @@ __device__ __forceinline__ void pc_tile(const FwdParams& p, const char* buf, con
   float ev[NJ][4];
   float etv[TT][NJ][4];
   float4 erow[ROWS ? T + 1 : 1][4];
+  // The compacted layout holds row jq of the item's query order at h * N * ceil4(N) +
+  // jq * ceil4(nk), keys in the item's key order (no gather through the site list).
+  const bool cmp = p.e_compact != 0;
+  const int nk4 = (nk + 3) & ~3;
+  const int eblk = N * ((N + 3) & ~3);
   if constexpr (HAS_E) {
-    const int64_t wstride = static_cast<int64_t>(N) * N * H;
+    const int64_t wstride = cmp ? static_cast<int64_t>(H) * eblk : static_cast<int64_t>(N) * N * H;
     const int64_t ebytes = wstride * 4;
     const __amdgpu_buffer_rsrc_t e_rs = make_rsrc(
         p.e != nullptr ? static_cast<const float*>(p.e) + b * wstride : nullptr, p.e != nullptr ? ebytes : 0);
@@ -515,21 +520,22 @@ __device__ __forceinline__ void pc_tile(const FwdParams& p, const char* buf, con
       for (int i = 0; i < 4; ++i) {
         const int cq = 4 * i + g;
         const int qs_i = __shfl(qsite, cq, 64);
-        const bool ok = tile * 16 + cq < nq && 4 * c < N;
-        const int off = ok ? static_cast<int>((qs_i * p.e_sq + h * p.e_sh) * 4) + 16 * c : e_oob;
+        const bool ok = tile * 16 + cq < nq && 4 * c < (cmp ? nk : N);
+        const int row = cmp ? h * eblk + (tile * 16 + cq) * nk4 : static_cast<int>(qs_i * p.e_sq + h * p.e_sh);
+        const int off = ok ? row * 4 + 16 * c : e_oob;
         erow[0][i] = buf_load4(e_rs, off);
 #pragma unroll
         for (int t = 0; t < T; ++t) erow[1 + t][i] = buf_load4(et_rsrc(t), off);
       }
     } else {
-      const int e_row = static_cast<int>(qsite * p.e_sq + h * p.e_sh);
+      const int e_row = cmp ? h * eblk + jq * nk4 : static_cast<int>(qsite * p.e_sq + h * p.e_sh);
 #pragma unroll
       for (int jt = 0; jt < NJ; ++jt)
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
           const int j = jt * 16 + 4 * r + g;
-          const int ks = key_all ? j : static_cast<int>(slot_perm[j & 63]);
-          const int eo = (j < nk && qvalid) ? (e_row + ks * static_cast<int>(p.e_sk)) * 4 : e_oob;
+          const int ks = cmp ? j : (key_all ? j : static_cast<int>(slot_perm[j & 63])) * static_cast<int>(p.e_sk);
+          const int eo = (j < nk && qvalid) ? (e_row + ks) * 4 : e_oob;
           ev[jt][r] = buf_load1(e_rs, eo);
 #pragma unroll
           for (int t = 0; t < T; ++t) etv[t][jt][r] = buf_load1(et_rsrc(t), eo);
@@ -666,7 +672,7 @@ __device__ __forceinline__ void pc_tile(const FwdParams& p, const char* buf, con
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
           const int j = jt * 16 + 4 * r + g;
-          const int ks = key_all ? j : static_cast<int>(slot_perm[j & 63]);
+          const int ks = (key_all || cmp) ? j : static_cast<int>(slot_perm[j & 63]);
           const float val = rg[c * kRF + ks];
           if (x == 0)
             ev[jt][r] = val;
@@ -1211,9 +1217,12 @@ constexpr bool pc_shape_ok() {
 }
 
 // Bias rows can be staged whole when a query's keys are contiguous and every row starts on a
-// 16-byte boundary (the [B, N, H, N] layout with N a multiple of 4, aligned base pointers).
+// 16-byte boundary (the [B, N, H, N] layout with N a multiple of 4, or the compacted layout;
+// aligned base pointers).
 bool e_rows_ok(const FwdParams& p) {
   auto aligned = [](const void* x) { return (reinterpret_cast<uintptr_t>(x) & 15) == 0; };
+  // compacted rows start at multiples of four floats whatever N
+  if (p.e_compact) return p.et_stride % 4 == 0 && aligned(p.e) && aligned(p.et);
   return p.e_sk == 1 && p.e_sq % 4 == 0 && p.e_sh % 4 == 0 && p.N % 4 == 0 && p.et_stride % 4 == 0 &&
          aligned(p.e) && aligned(p.et);
 }

@@ -35,6 +35,9 @@ struct FwdParams {
   // y_tstride elements between directions; lse is not written
   int gated;
   int64_t y_tstride;
+  // 1: e / et in the compacted physical-pair layout ([B, H, N, ceil4(N)] blocks of n rows of
+  // stride ceil4(n), the kernel's own query and key order); producer/consumer kernel only
+  int e_compact;
 };
 
 struct BwdParams {
@@ -186,6 +189,7 @@ struct PairBiasParams {
   int64_t B;
   int N;
   int64_t e_sq, e_sh, e_sk;
+  int64_t e_blk;        // > 0: compacted layout, floats per (walker, head) block (N * ceil4(N))
   float gain, eps, div;
   bool key_mask;        // compute every query row (key-mask attention semantics)
   int parts;            // items per walker (set by the launcher)

@@ -5,7 +5,10 @@
 //     h1  = h0 + gain * (silu(h0 W_1 + b_1) W_2 + b_2)
 //     e   = (h1 W_out + b_out) / div                    (H heads)
 // and, with a tangent edge_t, its forward-mode derivative, written straight into the
-// attention kernels' bias layout.
+// attention kernels' bias layout: [B, N, H, N] / [B, N, N, H], or the compacted layout
+// (e_blk > 0), where pair (i, j) of the walker's physical-site list goes to i * ceil4(n) + j
+// of head h's block, so the attention reads n * ceil4(n) contiguous floats per (walker, head)
+// instead of n rows of N.
 //
 // Orientation: every layer is computed transposed, features x pairs (features = the 16-row
 // M blocks, 16 pairs = one N block), so the pairs are the columns of the B operand and the
@@ -68,10 +71,12 @@ __device__ __forceinline__ float sigmoid(float u) {
   return __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(u * -1.44269504088896341f));
 }
 
-// The pairs of lane column c in tile t (N block cb): query site qi, key site qj, valid.
+// The pairs of lane column c in tile t (N block cb): query site qi, key site qj, valid, and
+// the pair's offset in a compacted (walker, head) block, row * ceil4(nk) + key (list order).
 template <bool TAN>
 __device__ __forceinline__ void tile_pairs(int t, int c, int npairs, int nk, bool rows_listed, bool keys_listed,
-                                           const unsigned short* list, int qi[2], int qj[2], bool valid[2]) {
+                                           const unsigned short* list, int qi[2], int qj[2], bool valid[2],
+                                           int cpos[2]) {
   constexpr int TP = TAN ? 16 : 32;
 #pragma unroll
   for (int cb = 0; cb < 2; ++cb) {
@@ -81,6 +86,7 @@ __device__ __forceinline__ void tile_pairs(int t, int c, int npairs, int nk, boo
     const int ii = qq / nk, jj = qq - ii * nk;
     qi[cb] = rows_listed ? list[ii] : ii;
     qj[cb] = keys_listed ? list[jj] : jj;
+    cpos[cb] = ii * ((nk + 3) & ~3) + jj;
   }
 }
 
@@ -189,16 +195,18 @@ __global__ void __launch_bounds__(256, (pb_occupancy<C, HB>())) pair_bias_kernel
 
     const float* edge_b = p.edge + b * pair_stride * C;
     const float* edge_tb = TAN ? p.edge_t + b * pair_stride * C : nullptr;
-    float* e_b = p.e + b * pair_stride * H;
-    float* et_b = TAN ? p.e_t + b * pair_stride * H : nullptr;
+    const bool cmp = p.e_blk > 0;
+    const int64_t wstride = cmp ? p.e_blk * H : pair_stride * H;
+    float* e_b = p.e + b * wstride;
+    float* et_b = TAN ? p.e_t + b * wstride : nullptr;
 
     // The edge rows of the item's first tile; each tile then loads the next tile's rows as
     // soon as its first layer has consumed its own, so the loads fly under layers 2-4.
-    int qi[2], qj[2];
+    int qi[2], qj[2], cpos[2];
     bool valid[2];
     float4 xin[2][CG];
     if (t0 < t1) {
-      tile_pairs<TAN>(t0, c, npairs, nk, rows_listed, keys_listed, list, qi, qj, valid);
+      tile_pairs<TAN>(t0, c, npairs, nk, rows_listed, keys_listed, list, qi, qj, valid, cpos);
       load_rows<C, TAN>(edge_b, edge_tb, N, g, qi, qj, valid, xin);
     }
     for (int t = t0; t < t1; ++t) {
@@ -240,10 +248,10 @@ __global__ void __launch_bounds__(256, (pb_occupancy<C, HB>())) pair_bias_kernel
       const float r0 = 1.0f / sqrtf(v0);
       // T = 1: the tangent's column scale rdot; T = 0: the second pair block's scale
       const float r1 = TAN ? (2.0f * s1 * inv_c) * (-0.5f * r0 / v0) : 1.0f / sqrtf(s1 * inv_c + p.eps);
-      int nqi[2] = {qi[0], qi[1]}, nqj[2] = {qj[0], qj[1]};
+      int nqi[2] = {qi[0], qi[1]}, nqj[2] = {qj[0], qj[1]}, ncpos[2] = {cpos[0], cpos[1]};
       bool nvalid[2] = {false, false};
       if (t + 1 < t1) {
-        tile_pairs<TAN>(t + 1, c, npairs, nk, rows_listed, keys_listed, list, nqi, nqj, nvalid);
+        tile_pairs<TAN>(t + 1, c, npairs, nk, rows_listed, keys_listed, list, nqi, nqj, nvalid, ncpos);
         load_rows<C, TAN>(edge_b, edge_tb, N, g, nqi, nqj, nvalid, xin);
       }
       v4f h0[4][2];
@@ -342,8 +350,8 @@ __global__ void __launch_bounds__(256, (pb_occupancy<C, HB>())) pair_bias_kernel
       for (int cb = 0; cb < 2; ++cb) {
         const int src = TAN ? 0 : cb;
         if (!valid[src]) continue;
-        float* dst = (TAN && cb == 1 ? et_b : e_b) + static_cast<int64_t>(qi[src]) * p.e_sq +
-                     static_cast<int64_t>(qj[src]) * p.e_sk;
+        float* const base = TAN && cb == 1 ? et_b : e_b;
+        float* dst = base + static_cast<int64_t>(qi[src]) * p.e_sq + static_cast<int64_t>(qj[src]) * p.e_sk;
         const bool with_bias = !(TAN && cb == 1);
 #pragma unroll
         for (int m = 0; m < HB; ++m) {
@@ -352,7 +360,10 @@ __global__ void __launch_bounds__(256, (pb_occupancy<C, HB>())) pair_bias_kernel
 #pragma unroll
           for (int r = 0; r < 4; ++r) val[r] = (o[m][cb][r] + (with_bias ? comp(bo, r) : 0.0f)) * inv_div;
           const int h = 16 * m + 4 * g;
-          if (p.e_sh == 1) {
+          if (cmp) {  // head h's block, the pair's compacted position
+#pragma unroll
+            for (int r = 0; r < 4; ++r) base[static_cast<int64_t>(h + r) * p.e_blk + cpos[src]] = val[r];
+          } else if (p.e_sh == 1) {
             *reinterpret_cast<float4*>(dst + h) = make_float4(val[0], val[1], val[2], val[3]);
           } else {
 #pragma unroll
@@ -364,6 +375,7 @@ __global__ void __launch_bounds__(256, (pb_occupancy<C, HB>())) pair_bias_kernel
       for (int cb = 0; cb < 2; ++cb) {
         qi[cb] = nqi[cb];
         qj[cb] = nqj[cb];
+        cpos[cb] = ncpos[cb];
         valid[cb] = nvalid[cb];
       }
     }

@@ -7,8 +7,9 @@ library is required.
 
 Layouts follow the reference primitives (``_pallas_attn/utils.py:21-36``):
 ``q, k, v: [B, N, H, D]``, ``e: [B, N, H, N]`` (or ``[B, N, N, H]`` with
-``e_layout="qkh"``), ``mask: [B, N]`` bool, ``lse: [B, N, H]`` float32, tangents
-``[T, B, N, H, D]`` or a single ``[B, N, H, D]`` direction.
+``e_layout="qkh"``, or the compacted physical-pair layout ``[B, H, N, ceil4(N)]`` with
+``e_layout="compact"``: ``compact_bias``), ``mask: [B, N]`` bool, ``lse: [B, N, H]`` float32,
+tangents ``[T, B, N, H, D]`` or a single ``[B, N, H, D]`` direction.
 
 Every call takes ``generic=True`` to force the LDS-streaming kernels (``HZ_FLAG_GENERIC``)
 instead of the automatic choice, for testing and comparison.
@@ -36,14 +37,60 @@ def _stream(device: torch.device) -> int:
     return torch.cuda.current_stream(device).cuda_stream
 
 
+E_LAYOUTS = ("qhk", "qkh", "compact")
+
+
+def e_shape(B: int, N: int, H: int, e_layout: str) -> tuple:
+    """Shape of the bias in ``e_layout``: ``[B, N, H, N]`` (query, head, key), ``[B, N, N, H]``
+    (``"qkh"``) or ``[B, H, N, ceil4(N)]`` (``"compact"``, see ``compact_bias``)."""
+    if e_layout == "qhk":
+        return (B, N, H, N)
+    if e_layout == "qkh":
+        return (B, N, N, H)
+    if e_layout == "compact":
+        return (B, H, N, (N + 3) // 4 * 4)
+    raise ValueError(f"e_layout must be one of {list(E_LAYOUTS)}, got {e_layout!r}")
+
+
 def _flags(key_mask: bool, e_layout: str, generic: bool = False) -> int:
-    if e_layout not in ("qhk", "qkh"):
-        raise ValueError(f"e_layout must be 'qhk' or 'qkh', got {e_layout!r}")
+    if e_layout not in E_LAYOUTS:
+        raise ValueError(f"e_layout must be one of {list(E_LAYOUTS)}, got {e_layout!r}")
     return (
         (_native.HZ_FLAG_KEY_MASK if key_mask else 0)
         | (_native.HZ_FLAG_E_QKH if e_layout == "qkh" else 0)
+        | (_native.HZ_FLAG_E_COMPACT if e_layout == "compact" else 0)
         | (_native.HZ_FLAG_GENERIC if generic else 0)
     )
+
+
+def compact_bias(e: Tensor, mask: Tensor, e_layout: str = "qhk") -> Tensor:
+    """The compacted physical-pair layout of a bias given in ``e_layout`` (``"qhk"`` or
+    ``"qkh"``), as ``hz_pair_bias`` writes it with ``HZ_FLAG_E_COMPACT``: ``[B, H, N, N4]``
+    (N4 = N rounded up to a multiple of 4) whose block ``(b, h)`` holds, for walker b's n
+    physical sites s_0 < ... < s_{n-1}, ``e[b, s_i, h, s_j]`` at flat position
+    ``i * ceil4(n) + j``; the rest is zero and never read. Square-mask attention only. A
+    layout conversion on the GPU (torch gather), for callers that hold a full bias."""
+    if e_layout not in ("qhk", "qkh"):
+        raise ValueError(f"e_layout must be 'qhk' or 'qkh', got {e_layout!r}")
+    B, N = e.shape[0], e.shape[1]
+    H = e.shape[2] if e_layout == "qhk" else e.shape[3]
+    eh = e if e_layout == "qhk" else e.permute(0, 1, 3, 2)  # [B, N(query), H, N(key)]
+    eh = eh.permute(0, 2, 1, 3)  # [B, H, Nq, Nk]
+    m = (mask.to(device=e.device) != 0)
+    # physical sites first, ascending (a stable sort of the inverted mask)
+    order = torch.sort((~m).to(torch.int8), dim=1, stable=True).indices  # [B, N]
+    g = torch.gather(eh, 2, order[:, None, :, None].expand(B, H, N, N))
+    g = torch.gather(g, 3, order[:, None, None, :].expand(B, H, N, N))
+    n = m.sum(dim=1)  # [B]
+    n4 = (n + 3) // 4 * 4
+    ar = torch.arange(N, device=e.device)
+    size = N * ((N + 3) // 4 * 4)
+    pos = ar[None, :, None] * n4[:, None, None] + ar[None, None, :]  # [B, i, j] -> i * ceil4(n) + j
+    valid = (ar[None, :, None] < n[:, None, None]) & (ar[None, None, :] < n[:, None, None])
+    pos = torch.where(valid, pos, torch.full_like(pos, size))  # invalid pairs land in a spare slot
+    out = torch.zeros((B, H, size + 1), dtype=e.dtype, device=e.device)
+    out.scatter_(2, pos.reshape(B, 1, N * N).expand(B, H, N * N), g.reshape(B, H, N * N))
+    return out[:, :, :size].reshape(e_shape(B, N, H, "compact")).contiguous()
 
 
 def _check_primals(q: Tensor, k: Tensor, v: Tensor, mask: Tensor, e: Optional[Tensor], e_layout: str):
@@ -66,7 +113,7 @@ def _check_primals(q: Tensor, k: Tensor, v: Tensor, mask: Tensor, e: Optional[Te
     if tuple(mask.shape) != (B, N):
         raise ValueError(f"mask.shape must be {(B, N)}, got {tuple(mask.shape)}")
     if e is not None:
-        want = (B, N, H, N) if e_layout == "qhk" else (B, N, N, H)
+        want = e_shape(B, N, H, e_layout)
         if tuple(e.shape) != want:
             raise ValueError(f"e.shape must be {want}, got {tuple(e.shape)}")
         if e.dtype != q.dtype:
@@ -107,12 +154,12 @@ def _tangent(t: Optional[Tensor], shape: tuple, dtype, name: str) -> Tuple[Optio
     return t.contiguous(), t.shape[0]
 
 
-def _tangents(q, e_shape, qt, kt, et, vt):
+def _tangents(q, eshape, qt, kt, et, vt):
     shape = tuple(q.shape)
     qt, tq = _tangent(qt, shape, q.dtype, "qt")
     kt, tk = _tangent(kt, shape, q.dtype, "kt")
     vt, tv = _tangent(vt, shape, q.dtype, "vt")
-    et, te = _tangent(et, e_shape, q.dtype, "et")
+    et, te = _tangent(et, eshape, q.dtype, "et")
     _on_device(q.device, qt=qt, kt=kt, vt=vt, et=et)
     counts = {x for x in (tq, tk, tv, te) if x}
     if len(counts) > 1:
@@ -173,9 +220,9 @@ def mhsea_jvp(
     zero tangent. Returns ``tout`` shaped like the given tangents.
     """
     B, N, H, D = _check_primals(q, k, v, mask, e, e_layout)
-    e_shape = (B, N, H, N) if e_layout == "qhk" else (B, N, N, H)
+    e_shape_ = e_shape(B, N, H, e_layout)
     batched = any(t is not None and t.dim() == 5 for t in (qt, kt, vt)) or (et is not None and et.dim() == 5)
-    qt, kt, et, vt, T = _tangents(q, e_shape, qt, kt, et, vt)
+    qt, kt, et, vt, T = _tangents(q, e_shape_, qt, kt, et, vt)
     if tuple(out.shape) != (B, N, H, D) or out.dtype != q.dtype:
         raise ValueError("out must match q in shape and dtype")
     if tuple(lse.shape) != (B, N, H) or lse.dtype != torch.float32:
@@ -213,9 +260,9 @@ def mhsea_fwd_jvp(
 ) -> Tuple[Tensor, Optional[Tensor], Tensor]:
     """Fused forward + tangents: returns ``(out, lse, tout)`` in one pass over K/V."""
     B, N, H, D = _check_primals(q, k, v, mask, e, e_layout)
-    e_shape = (B, N, H, N) if e_layout == "qhk" else (B, N, N, H)
+    e_shape_ = e_shape(B, N, H, e_layout)
     batched = any(t is not None and t.dim() == 5 for t in (qt, kt, vt)) or (et is not None and et.dim() == 5)
-    qt, kt, et, vt, T = _tangents(q, e_shape, qt, kt, et, vt)
+    qt, kt, et, vt, T = _tangents(q, e_shape_, qt, kt, et, vt)
     q, k, v, e = _c(q), _c(k), _c(v), _c(e)
     m = _mask_u8(mask, q.device)
     out = torch.empty_like(q)
@@ -258,12 +305,12 @@ def mhsea_fwd_jvp_gated(
         raise TypeError(f"the gated collapse computes in float32, got {q.dtype}")
     if H % 2:
         raise ValueError(f"the gated collapse pairs head h with h + H/2: H must be even, got {H}")
-    e_shape = (B, N, H, N) if e_layout == "qhk" else (B, N, N, H)
+    e_shape_ = e_shape(B, N, H, e_layout)
     if all(t is None for t in (qt, kt, vt, et)):
         T, batched = 0, False
     else:
         batched = any(t is not None and t.dim() == 5 for t in (qt, kt, vt)) or (et is not None and et.dim() == 5)
-        qt, kt, et, vt, T = _tangents(q, e_shape, qt, kt, et, vt)
+        qt, kt, et, vt, T = _tangents(q, e_shape_, qt, kt, et, vt)
     q, k, v, e = _c(q), _c(k), _c(v), _c(e)
     m = _mask_u8(mask, q.device)
     y = torch.empty((B, N, H // 2, D), dtype=q.dtype, device=q.device)
@@ -390,8 +437,8 @@ def mhsea_bwd(
     dq = torch.empty_like(q)
     dk = torch.empty_like(q)
     dv = torch.empty_like(q)
-    e_shape = (B, N, H, N) if e_layout == "qhk" else (B, N, N, H)
-    de = torch.empty(e_shape, dtype=q.dtype, device=q.device) if want_de else None
+    e_shape_ = e_shape(B, N, H, e_layout)
+    de = torch.empty(e_shape_, dtype=q.dtype, device=q.device) if want_de else None
     _native.check(
         _native.lib().hz_mhsea_bwd(
             _stream(q.device), _ptr(q), _ptr(k), _ptr(e), _ptr(v), _ptr(m), _ptr(lse), _ptr(out),

@@ -9,9 +9,10 @@ Reference: ``MultiHeadEvenAttention.__call__`` (``src/hamiltonzero/model/trunk.p
     coup_bias = coup_bias / sqrt(d_head)
 
 ``coupling_bias`` runs all three in one launch of ``hz_pair_bias`` (``include/hz_pair_bias.h``)
-and writes the result straight into the attention's bias layout (``[B, N, H, N]``, or the
-reference's ``[B, N, N, H]`` with ``e_layout="qkh"``), with the forward-mode tangent along
-``edge_t`` when given. There is no CPU fallback: the HIP library is required and every
+and writes the result straight into the attention's bias layout (``[B, N, H, N]``, the
+reference's ``[B, N, N, H]`` with ``e_layout="qkh"``, or the compacted physical-pair layout
+that the N <= 64 attention kernel reads most cheaply, ``e_layout="compact"``:
+``kernels.compact_bias``), with the forward-mode tangent along ``edge_t`` when given. There is no CPU fallback: the HIP library is required and every
 operand must be a float32 CUDA tensor on one device.
 
 Parameters use the reference's names, flattened: ``ln_w`` (``ln_edge.weight``), ``w_in`` /
@@ -26,7 +27,7 @@ from typing import Mapping, Optional, Tuple, Union
 
 import torch
 
-from . import _native
+from . import _native, kernels
 
 Tensor = torch.Tensor
 
@@ -65,12 +66,15 @@ def coupling_bias(
     axis for a single direction). ``inner_gain`` is the MLP's ``n_layers ** -0.5``
     (``trunk.py:61``). With ``mask [B, N]`` only the pairs the attention reads are computed
     (see ``include/hz_pair_bias.h``; ``key_mask`` as in the attention call) and the others
-    are zero.
+    are zero. ``e_layout="compact"`` (square mask only) writes the layout of
+    ``kernels.compact_bias``.
     """
     if edge.dim() != 4 or edge.shape[1] != edge.shape[2]:
         raise ValueError(f"edge must be [B, N, N, C], got {tuple(edge.shape)}")
-    if e_layout not in ("qhk", "qkh"):
-        raise ValueError(f"e_layout must be 'qhk' or 'qkh', got {e_layout!r}")
+    if e_layout not in kernels.E_LAYOUTS:
+        raise ValueError(f"e_layout must be one of {list(kernels.E_LAYOUTS)}, got {e_layout!r}")
+    if e_layout == "compact" and key_mask:
+        raise ValueError("e_layout='compact' serves the square mask only (key_mask=False)")
     B, N, _, C = edge.shape
     if C not in EDGE_CHANNELS:
         raise ValueError(f"edge channels must be one of {list(EDGE_CHANNELS)}, got {C}")
@@ -95,12 +99,12 @@ def coupling_bias(
         single = edge_t.dim() == 4
         tangents = edge_t.unsqueeze(0) if single else edge_t
         tangents = _check("edge_t", tangents, dev, (tangents.shape[0], B, N, N, C))
-    eshape = (B, N, H, N) if e_layout == "qhk" else (B, N, N, H)
+    eshape = kernels.e_shape(B, N, H, e_layout)
     alloc = torch.zeros if m is not None else torch.empty
     e = alloc(eshape, dtype=torch.float32, device=dev)
     T = 0 if tangents is None else tangents.shape[0]
     e_t = alloc((T, *eshape), dtype=torch.float32, device=dev) if T else None
-    flags = (_native.HZ_FLAG_KEY_MASK if key_mask else 0) | (_native.HZ_FLAG_E_QKH if e_layout == "qkh" else 0)
+    flags = kernels._flags(key_mask, e_layout)
     lib = _native.lib()
     stream = torch.cuda.current_stream(dev).cuda_stream
     div = float(torch.sqrt(torch.tensor(float(d_head), dtype=torch.float32)))  # jnp.sqrt in float32

@@ -24,6 +24,14 @@
  *                                        [B, N, N, H]  with HZ_FLAG_E_QKH (op-level layout,
  *                                        pallas_attention.py:45, so no transpose pass)
  *      et                              : [T, <layout of e>]
+ *      e (compact, HZ_FLAG_E_COMPACT)  : [B, H, N, N4], N4 = N rounded up to a multiple of 4:
+ *                                        block (b, h) holds the bias of the n x n physical
+ *                                        pairs of walker b (n = its physical site count,
+ *                                        sites in ascending order on both sides) as n rows
+ *                                        of stride n4 = n rounded up to 4, i.e. entry
+ *                                        (i, j) at i * n4 + j; the rest is never read.
+ *                                        The forward family reads only these n * n4 floats
+ *                                        per (walker, head). hz_pair_bias writes it.
  *      mask                            : [B, N] uint8 (0 = padded/virtual site, else physical)
  *      lse                             : [B, N, H] float32 (natural log-sum-exp per query row)
  *  - dtype: HZ_DTYPE_F32 (all float tensors float32) or HZ_DTYPE_BF16 (q, k, v, e, all
@@ -76,7 +84,12 @@ enum hz_dtype { HZ_DTYPE_F32 = 0, HZ_DTYPE_BF16 = 1 };
 enum hz_flags {
   HZ_FLAG_KEY_MASK = 1, /* reference_edge_attention masking instead of the square mask */
   HZ_FLAG_E_QKH = 2,    /* e / et / de are [B, N(query), N(key), H] */
-  HZ_FLAG_GENERIC = 4   /* always use the LDS-streaming kernels (testing / comparison) */
+  HZ_FLAG_GENERIC = 4,  /* always use the LDS-streaming kernels (testing / comparison) */
+  /* e / et in the compacted physical-pair layout (above). Square mask only (not with
+     HZ_FLAG_KEY_MASK), float32, and only where the N <= 64 producer/consumer kernel serves
+     the shape (N <= 64, D in {8, 16, 32}); accepted by hz_mhsea_fwd, hz_mhsea_jvp,
+     hz_mhsea_fwd_jvp and hz_mhsea_fwd_jvp_gated, refused (HZ_EINVAL) elsewhere. */
+  HZ_FLAG_E_COMPACT = 8
 };
 
 enum hz_status {

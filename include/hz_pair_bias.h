@@ -27,6 +27,13 @@
  * 1 <= N <= HZ_MAX_N, B >= 1, T in {0, 1}. inner_gain = n_layers^-1/2 (trunk.py:61),
  * eps = 1e-5 (odd_ops.py:185), bias_div = sqrt(d_head) (trunk.py:103-105).
  *
+ * HZ_FLAG_E_COMPACT (hz_mhsea.h): e / e_t in the compacted physical-pair layout [B, H, N,
+ * ceil4(N)] that the N <= 64 forward family reads with the same flag — pair (i, j) of the
+ * walker's ascending physical-site list at i * ceil4(n) + j of head h's block, so the rows are
+ * contiguous and hold only the pairs the attention reads. Square mask only (not with
+ * HZ_FLAG_KEY_MASK or HZ_FLAG_E_QKH); with a mask, N <= 256; with mask == NULL every site
+ * counts as physical.
+ *
  * Mask: with mask != NULL and N <= 256 only the pairs the attention reads are computed and
  * written — keys with mask[j] != 0, and queries with mask[i] != 0 unless HZ_FLAG_KEY_MASK
  * (whose attention computes every query row); in key-mask mode a walker with no physical

@@ -61,6 +61,13 @@ def _fwd(lib, **over):
         (dict(out=None), _native.HZ_ENULL, "out"),
         (dict(v=A + 4), _native.HZ_EALIGN, "aligned"),
         (dict(scale=float("nan")), _native.HZ_EINVAL, "scale"),
+        # the compacted bias layout: square mask, float32, the N <= 64 kernel's shapes
+        (dict(flags=8 | 1), _native.HZ_EINVAL, "excludes HZ_FLAG_KEY_MASK"),
+        (dict(flags=8 | 2), _native.HZ_EINVAL, "excludes"),
+        (dict(flags=8 | 4), _native.HZ_EINVAL, "excludes"),
+        (dict(flags=8, D=64), _native.HZ_EINVAL, "HZ_FLAG_E_COMPACT needs"),
+        (dict(flags=8, N=65), _native.HZ_EINVAL, "HZ_FLAG_E_COMPACT needs"),
+        (dict(flags=8, dtype=1), _native.HZ_EINVAL, "HZ_FLAG_E_COMPACT needs"),
     ],
 )
 def test_fwd_rejects_bad_arguments(lib, over, code, needle):
@@ -89,6 +96,19 @@ def test_bwd_rejects_missing_cotangent_outputs(lib):
     assert rc == _native.HZ_ENULL and "dk" in lib.hz_last_error().decode()
     rc = lib.hz_mhsea_bwd(None, A, A, None, A, A, A, A, A, A, A, A + 8, A, 2, 64, 8, 32, 0, 1.0, 0)
     assert rc == _native.HZ_EALIGN and "de" in lib.hz_last_error().decode()
+
+
+def test_compact_bias_layout_is_refused_outside_the_forward_family(lib):
+    rc = lib.hz_mhsea_bwd(None, A, A, A, A, A, A, A, A, A, A, A, A, 2, 64, 8, 32, 0, 1.0, 8)
+    assert rc == _native.HZ_EINVAL and "forward family" in lib.hz_last_error().decode()
+    # stream, edge, edge_t, mask, ln_w, w_in, b_in, w_1, b_1, w_2, b_2, w_out, b_out, e, e_t,
+    # B, N, C, hidden, H, T, inner_gain, eps, bias_div, flags
+    pb = [None] + [A] * 14 + [2, 64, 96, 64, 32, 1, 0.5, 1e-5, 4.0]
+    assert lib.hz_pair_bias(*pb, 8 | 1) == _native.HZ_EINVAL
+    assert "excludes HZ_FLAG_KEY_MASK" in lib.hz_last_error().decode()
+    pb_large = [None] + [A] * 14 + [2, 300, 96, 64, 32, 1, 0.5, 1e-5, 4.0]
+    assert lib.hz_pair_bias(*pb_large, 8) == _native.HZ_EINVAL
+    assert "N <= 256" in lib.hz_last_error().decode()
 
 
 def test_error_string_is_thread_local(lib):
