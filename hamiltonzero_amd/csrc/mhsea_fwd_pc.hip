@@ -862,17 +862,21 @@ __device__ __forceinline__ void pc_tile(const FwdParams& p, const char* buf, con
 // v_mfma_f32_4x4x1_16b_f32 (sixteen independent 4x4 outer products per instruction, the same
 // flops per cycle) does the tile's work at a third of the matrix-core time.
 //   S^T: one instruction per feature d; lane l supplies A = K[key l][d] and B = Q[query
-//   l & 3][d] (one ds_bpermute from the lane of the query fragments holding it), so lane
-//   4m + j accumulates the scores of keys 4m .. 4m+3 (registers 0-3) for query j. The softmax
-//   reduces over the 16 lanes of a query (lane bits 2-5).
+//   l & 3][d], so lane 4m + j accumulates the scores of keys 4m .. 4m+3 (registers 0-3) for
+//   query j. The four query rows reach every lane through a small LDS region (written from
+//   the query fragments, read back as 16-byte rows). The softmax reduces over the 16 lanes of a
+//   query (lane bits 2-5).
 //   O^T = V^T P^T, A^T, C^T: block b = 8 part + dg covers features 4dg .. 4dg+3; the keys are
 //   cut into two parts of 4 H4 (H4 = ceil(nk / 8) groups of 4), and in step (m, r) block b
 //   takes key 4 (part H4 + m) + r: lane l supplies A = V[key][l mod 32] and B = P[query
-//   l & 3][key] (one ds_bpermute from the lane holding it in register r). Lane 32 part + 4dg + j
-//   then holds features 4dg .. 4dg+3 of query j for its part; the parts are added across lane
-//   bit 5. Keys nk .. 8 H4 - 1 read rows the producer zero-fills (8 H4 <= the 16-row padded
-//   count) and carry P = 0.
-// Served for D = 32, the plain forward (+ tangents) without bias.
+//   l & 3][key]. The weights go through the same LDS region, so one 16-byte read gives a lane
+//   the four keys of its steps (m, 0..3) (gathering them by ds_bpermute, one per step, made the
+//   c2 step 1.5% slower). Lane 32 part + 4dg + j then holds features 4dg .. 4dg+3 of query j for
+//   its part; the parts are added across lane bit 5. Keys nk .. 8 H4 - 1 read rows the
+//   producer zero-fills (8 H4 <= the 16-row padded count) and carry P = 0.
+// Served for D = 32, the plain forward (+ tangents) without bias; the LDS region holds
+// (1 + T) x (4 query rows + 4 x 64 weights) floats, one per workgroup (one remainder tile per
+// item).
 __device__ __forceinline__ v4f mfma4x4(float a, float b, v4f c) {
   return __builtin_amdgcn_mfma_f32_4x4x1f32(a, b, c, 0, 0, 0);
 }
@@ -896,7 +900,7 @@ __device__ __forceinline__ float query_sum(float x) {
 
 template <int D, int T, class PF, class SQ>
 __device__ __forceinline__ void pc_tile_rem4(const FwdParams& p, const char* buf, const QSet<D, T>& qs, int tile,
-                                             PF&& pf, SQ&& sq) {
+                                             PF&& pf, SQ&& sq, float* rl) {
   static_assert(D == 32, "four-query remainder tile: D = 32");
   using Sh = PcShape<D, T>;
   constexpr int DG = Sh::DG, TT = Sh::TT;
@@ -933,20 +937,50 @@ __device__ __forceinline__ void pc_tile_rem4(const FwdParams& p, const char* buf
       ktv[t][4 * c + 3] = y.w;
     }
   }
+  // the four query rows (and tangents) through LDS: lanes (g, c < 4) write their fragments,
+  // every lane reads its query's row (the wave's LDS accesses complete in order)
+  {
+    const int g = lane >> 4, c = lane & 15;
+    if (c < 4) {
+#pragma unroll
+      for (int s4 = 0; s4 < DG; s4 += 4) {
+        *reinterpret_cast<float4*>(rl + c * D + g * DG + s4) =
+            make_float4(qs.qf[s4], qs.qf[s4 + 1], qs.qf[s4 + 2], qs.qf[s4 + 3]);
+#pragma unroll
+        for (int t = 0; t < T; ++t)
+          *reinterpret_cast<float4*>(rl + (1 + t) * 4 * D + c * D + g * DG + s4) =
+              make_float4(qs.qtf[t][s4], qs.qtf[t][s4 + 1], qs.qtf[t][s4 + 2], qs.qtf[t][s4 + 3]);
+      }
+    }
+  }
+  float qrow[D], qtrow[TT][D];
+#pragma unroll
+  for (int d4 = 0; d4 < D; d4 += 4) {
+    const float4 x = *reinterpret_cast<const float4*>(rl + j * D + d4);
+    qrow[d4] = x.x;
+    qrow[d4 + 1] = x.y;
+    qrow[d4 + 2] = x.z;
+    qrow[d4 + 3] = x.w;
+#pragma unroll
+    for (int t = 0; t < T; ++t) {
+      const float4 y = *reinterpret_cast<const float4*>(rl + (1 + t) * 4 * D + j * D + d4);
+      qtrow[t][d4] = y.x;
+      qtrow[t][d4 + 1] = y.y;
+      qtrow[t][d4 + 2] = y.z;
+      qtrow[t][d4 + 3] = y.w;
+    }
+  }
   v4f sc = zero4();
   v4f ds[TT];
 #pragma unroll
   for (int t = 0; t < TT; ++t) ds[t] = zero4();
 #pragma unroll
   for (int d = 0; d < D; ++d) {
-    const int src = (d / DG) * 16 + j;  // lane (g, c = j) of the fragments holds Q[j][d] at d % DG
-    const float qd = __shfl(qs.qf[d % DG], src, 64);
-    sc = mfma4x4(kv[d], qd, sc);
+    sc = mfma4x4(kv[d], qrow[d], sc);
 #pragma unroll
     for (int t = 0; t < T; ++t) {
-      const float qtd = __shfl(qs.qtf[t][d % DG], src, 64);
-      ds[t] = mfma4x4(ktv[t][d], qd, ds[t]);
-      ds[t] = mfma4x4(kv[d], qtd, ds[t]);
+      ds[t] = mfma4x4(ktv[t][d], qrow[d], ds[t]);
+      ds[t] = mfma4x4(kv[d], qtrow[t][d], ds[t]);
     }
   }
 
@@ -979,25 +1013,32 @@ __device__ __forceinline__ void pc_tile_rem4(const FwdParams& p, const char* buf
   const int part = lane >> 5;
   const int h4 = (nk + 7) >> 3;
   const int dcol = lane & 31;
+  // weights through LDS: lane 4m + j holds P[j][4m .. 4m + 3] (and P o dS): one 16-byte write
+  // each, then one 16-byte read per key group gives a lane its four keys of a step
+  float* const pl = rl + (1 + T) * 4 * D;  // [(1 + T)][4 queries][64 keys]
+  *reinterpret_cast<v4f*>(pl + j * 64 + 4 * (lane >> 2)) = sc;
+#pragma unroll
+  for (int t = 0; t < T; ++t) *reinterpret_cast<v4f*>(pl + (1 + t) * 256 + j * 64 + 4 * (lane >> 2)) = ds[t];
   v4f o = zero4();
   v4f at[TT], ct[TT];
 #pragma unroll
   for (int t = 0; t < TT; ++t) at[t] = ct[t] = zero4();
   for (int m = 0; m < h4; ++m) {
     const int grp = part * h4 + m;
-    const int src = 4 * grp + j;
+    const v4f p4 = *reinterpret_cast<const v4f*>(pl + j * 64 + 4 * grp);
+    v4f d4[TT];
+#pragma unroll
+    for (int t = 0; t < T; ++t) d4[t] = *reinterpret_cast<const v4f*>(pl + (1 + t) * 256 + j * 64 + 4 * grp);
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
       const int off = swz_off<D>(4 * grp + r, dcol >> 2) + (dcol & 3) * 4;
       const float vv = *reinterpret_cast<const float*>(V0 + off);
-      const float pv = __shfl(sc[r], src, 64);
-      o = mfma4x4(vv, pv, o);
+      o = mfma4x4(vv, p4[r], o);
 #pragma unroll
       for (int t = 0; t < T; ++t) {
-        const float pd = __shfl(ds[t][r], src, 64);
         const float vt = *reinterpret_cast<const float*>(V0 + (1 + t) * Sh::TILE + off);
-        at[t] = mfma4x4(vv, pd, at[t]);
-        ct[t] = mfma4x4(vt, pv, ct[t]);
+        at[t] = mfma4x4(vv, d4[t][r], at[t]);
+        ct[t] = mfma4x4(vt, p4[r], ct[t]);
       }
     }
   }
@@ -1053,6 +1094,8 @@ __device__ __forceinline__ void pc_consumer(const FwdParams& p, char* lds, const
   const int N = p.N;
   const bool km = p.key_mask != 0;
   const char* const slots = lds + 2 * Sh::BUF;
+  // the four-query remainder tile's LDS region (one per workgroup: one remainder tile per item)
+  float* const rem_lds = reinterpret_cast<float*>(lds + Sh::LDS + (EM == 2 ? PcEStage<D, T>::BYTES : 0));
   auto slot_perm = [&](int k) { return reinterpret_cast<const int16_t*>(slots + (k % kSlots) * kSlotBytes); };
   auto slot_n = [&](int k) { return reinterpret_cast<const int*>(slots + (k % kSlots) * kSlotBytes + 128)[0]; };
 
@@ -1083,7 +1126,7 @@ __device__ __forceinline__ void pc_consumer(const FwdParams& p, char* lds, const
     // Remainder tiles of at most four queries take the 4x4-block path where it is built.
     constexpr bool kRem4 = D == 32 && !GIVEN_LSE && EM == 0 && R == 0;
     if (kRem4 && wave * 16 < nq && nq - wave * 16 <= 4) {
-      if constexpr (kRem4) pc_tile_rem4<D, T>(p, buf, qs, wave, pf, sq);
+      if constexpr (kRem4) pc_tile_rem4<D, T>(p, buf, qs, wave, pf, sq, rem_lds);
     } else if (wave * 16 < nq) {
       switch ((nk + 15) >> 4) {
         case 1: pc_tile<D, T, GIVEN_LSE, EM, 1, R>(p, buf, sp, qs, wave, pf, sq, gm, estage); break;
@@ -1101,7 +1144,7 @@ __device__ __forceinline__ void pc_consumer(const FwdParams& p, char* lds, const
       QSet<D, T> q3;
       pc_load_q<D, T, GIVEN_LSE>(p, q3, qs.b, qs.h, qs.n_phys, sp, 3);
       if (kRem4 && nq - 3 * 16 <= 4) {
-        if constexpr (kRem4) pc_tile_rem4<D, T>(p, buf, q3, 3, [] {}, [] {});
+        if constexpr (kRem4) pc_tile_rem4<D, T>(p, buf, q3, 3, [] {}, [] {}, rem_lds);
       } else {
         switch ((nk + 15) >> 4) {
           case 1: pc_tile<D, T, GIVEN_LSE, EM, 1, R>(p, buf, sp, q3, 3, [] {}, [] {}, gx, estage); break;
@@ -1183,7 +1226,8 @@ hipError_t launch_pc_t(const FwdParams& p, hipStream_t stream) {
   using Sh = PcShape<D, T>;
   static_assert(EM != 2 || PcEStage<D, T>::OK, "two workgroups per CU");
   auto kern = mhsea_fwd_pc_kernel<D, T, GIVEN_LSE, EM, GATED>;
-  const size_t lds = Sh::LDS + (EM == 2 ? PcEStage<D, T>::BYTES : 0);
+  constexpr bool kRem4Lds = D == 32 && !GIVEN_LSE && EM == 0 && !GATED;
+  const size_t lds = Sh::LDS + (EM == 2 ? PcEStage<D, T>::BYTES : 0) + (kRem4Lds ? (1 + T) * (4 * D + 256) * 4 : 0);
   if (lds > 64 * 1024) {
     hipError_t err = hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
                                          hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(lds));
