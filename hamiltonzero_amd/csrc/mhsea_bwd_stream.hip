@@ -390,14 +390,18 @@ __global__ void __launch_bounds__(256, ((ROWS && D == 32) ? 2 : BwdStreamShape<D
       const bool key_all = km && sc_.n_phys == 0;
       const int nmask = N - sc_.n_phys;
       if (!key_all) {
-        for (int base = 0; base < nmask * C4; base += 256) {
-          const int it = base + tid;
-          const int site = __shfl(sc_.perm, (sc_.n_phys + it / C4) & 63, 64);
-          if (it < nmask * C4) {
-            const int64_t off = bnhd(bc, site, hc, N, H, D) + (it % C4) * 4;
-            if (!km) store4<S>(p.dq, off, 0.f, 0.f, 0.f, 0.f);
-            store4<S>(p.dk, off, 0.f, 0.f, 0.f, 0.f);
-            store4<S>(p.dv, off, 0.f, 0.f, 0.f, 0.f);
+        // item (b, h) zeroes the masked sites i = h, h + H, ... of its walker for every head,
+        // each site's [H, D] rows as one contiguous run (the walker's H items cover every
+        // masked site once; per-item 128-byte rows at a stride of H D cost the forward 2.6%)
+        const int F = H * C4;
+        const int nmine = nmask > hc ? (nmask - hc + H - 1) / H : 0;
+        for (int si = static_cast<int>(threadIdx.x >> 6); si < nmine; si += 4) {  // a site per wave
+          const int site = __builtin_amdgcn_readlane(sc_.perm, (sc_.n_phys + hc + si * H) & 63);
+          const int64_t base = bnhd(bc, site, 0, N, H, D);
+          for (int w = static_cast<int>(threadIdx.x & 63); w < F; w += 64) {
+            if (!km) store4<S>(p.dq, base + 4 * w, 0.f, 0.f, 0.f, 0.f);
+            store4<S>(p.dk, base + 4 * w, 0.f, 0.f, 0.f, 0.f);
+            store4<S>(p.dv, base + 4 * w, 0.f, 0.f, 0.f, 0.f);
           }
         }
       }

@@ -406,17 +406,21 @@ __global__ void __launch_bounds__(256, (StreamShape<D, T>::kWavesPerEu))
 
     // ---- rows of masked queries (square mask): exact zeros, lse = -1e4 + log N ---------
     if (!p.key_mask) {
+      // item (b, h) writes the masked sites i = h, h + H, ... of its walker for every head,
+      // each site's [H, D] rows as one contiguous run (the walker's H items cover every
+      // masked site once)
       const int nmask = N - sc_.n_phys;
-      for (int base = 0; base < nmask * C4; base += 256) {
-        const int it = base + tid;
-        const int site = __shfl(sc_.perm, (sc_.n_phys + it / C4) & 63, 64);
-        if (it < nmask * C4) {
-          const int64_t off = bnhd(bc, site, hc, N, H, D) + (it % C4) * 4;
-          if constexpr (!GIVEN_LSE) store4<S>(p.out, off, 0.f, 0.f, 0.f, 0.f);
+      const int F = H * C4;
+      const int nmine = nmask > hc ? (nmask - hc + H - 1) / H : 0;
+      for (int si = static_cast<int>(threadIdx.x >> 6); si < nmine; si += 4) {  // a site per wave
+        const int site = __builtin_amdgcn_readlane(sc_.perm, (sc_.n_phys + hc + si * H) & 63);
+        const int64_t base = bnhd(bc, site, 0, N, H, D);
+        for (int w = static_cast<int>(threadIdx.x & 63); w < F; w += 64) {
+          if constexpr (!GIVEN_LSE) store4<S>(p.out, base + 4 * w, 0.f, 0.f, 0.f, 0.f);
 #pragma unroll
-          for (int t = 0; t < T; ++t) store4<S>(p.tout, t * p.t_stride + off, 0.f, 0.f, 0.f, 0.f);
-          if (!GIVEN_LSE && it % C4 == 0 && p.lse != nullptr)
-            p.lse[(static_cast<int64_t>(bc) * N + site) * H + hc] = p.masked_lse;
+          for (int t = 0; t < T; ++t) store4<S>(p.tout, t * p.t_stride + base + 4 * w, 0.f, 0.f, 0.f, 0.f);
+          if (!GIVEN_LSE && w < H && p.lse != nullptr)
+            p.lse[(static_cast<int64_t>(bc) * N + site) * H + w] = p.masked_lse;
         }
       }
     }
