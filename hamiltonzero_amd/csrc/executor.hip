@@ -620,9 +620,15 @@ hipError_t launch_factorized_apply(const float* x, const float* V, const float* 
 
 hipError_t launch_out_proj(const float* y, const float* w_o, const uint8_t* mask, float* delta, int64_t M, int d_in,
                            int d_out, hipStream_t stream) {
-  if (mask != nullptr && d_out % 4 == 0 && d_in % 4 == 0) {
-    const int64_t ncol = (d_out + kBN - 1) / kBN;
-    const int64_t blocks = ncol * ((M + kRM - 1) / kRM);
+  // The row-compacting kernel where its 256-row workgroups fill the chip; below that (few
+  // rows, e.g. one large-N system's 4096 query rows: 64 workgroups for 256 CUs) the 128 x 128
+  // tiled GEMM with the row mask in its epilogue runs twice the workgroups and multiplies the
+  // masked rows too (the large-N tail's W_O on 4096 rows: about 93 -> 53 us).
+  int cus = 0;
+  if (hipError_t err = device_cu_count(&cus); err != hipSuccess) return err;
+  const int64_t ncol = (d_out + kBN - 1) / kBN;
+  const int64_t blocks = ncol * ((M + kRM - 1) / kRM);
+  if (mask != nullptr && d_out % 4 == 0 && d_in % 4 == 0 && blocks >= cus) {
     if (blocks > 0x7fffffffLL) return hipErrorInvalidValue;
     hipLaunchKernelGGL(gemm_rows_f32_kernel, dim3(static_cast<unsigned>(blocks)), dim3(256), 0, stream, y, w_o, delta,
                        mask, M, d_out, d_in, static_cast<int>(ncol));
