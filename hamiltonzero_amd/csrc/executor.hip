@@ -287,11 +287,16 @@ gemm_rows_f32_kernel(const float* __restrict__ A, const float* __restrict__ Bm, 
   if (valid && !phys) mrow[mbase + __popcll(mb & below)] = static_cast<int16_t>(tid);
   __syncthreads();
 
-  // masked rows of this column tile: zeros, 16 bytes per store
-  for (int i = tid; i < nm * (kBN / 4); i += 256) {
-    const int col = n0 + 4 * (i % (kBN / 4));
-    if (col < N)
-      *reinterpret_cast<float4*>(C + (m0 + mrow[i / (kBN / 4)]) * N + col) = make_float4(0.f, 0.f, 0.f, 0.f);
+  // masked rows: the workgroup of column tile t writes the whole rows (every column) of the
+  // masked rows i = t, t + ncol, ... of its row block, each row one contiguous run
+  {
+    const int t = static_cast<int>(L % ncol);
+    const int nmine = nm > t ? (nm - t + ncol - 1) / ncol : 0;
+    const int n4 = N / 4;
+    for (int i = tid; i < nmine * n4; i += 256) {
+      const int mi = t + (i / n4) * ncol;
+      *reinterpret_cast<float4*>(C + (m0 + mrow[mi]) * N + 4 * (i % n4)) = make_float4(0.f, 0.f, 0.f, 0.f);
+    }
   }
   if (n == 0) return;  // workgroup-uniform
 
