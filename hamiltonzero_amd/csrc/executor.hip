@@ -130,10 +130,19 @@ enum GemmEpi { kEpiPlain = 0, kEpiCond = 1, kEpiResidual = 2, kEpiRowMask = 3 };
 // C may be the residual itself (each output entry reads its residual entry, then overwrites
 // it, in one thread), so neither carries __restrict__. VEC: K and N are multiples of 4
 // (16-byte staging loads); otherwise the staging loads are per element.
+// Split K (gridDim.z > 1): workgroup z contracts k in [z K, min(z K + K, Ktot)) of A (row
+// stride lda) and B and writes its partial product (EPI plain) at C + z cz.
 template <int EPI, bool VEC>
 __global__ void __launch_bounds__(256, 2)
 gemm_f32_kernel(const float* __restrict__ A, const float* __restrict__ Bm, float* C, const float* aux, int64_t M, int N,
-                int K, int h_rows, int64_t row0) {
+                int K, int h_rows, int64_t row0, int lda, int Ktot, int64_t cz) {
+  {
+    const int kbeg = static_cast<int>(blockIdx.z) * K;
+    A += kbeg;
+    Bm += static_cast<int64_t>(kbeg) * N;
+    C += static_cast<int64_t>(blockIdx.z) * cz;
+    K = Ktot - kbeg < K ? Ktot - kbeg : K;
+  }
   __shared__ float As[2][kBK][kAPad];
   __shared__ float Bs[2][kBK][kBPad];
   const int tid = threadIdx.x;
@@ -153,10 +162,10 @@ gemm_f32_kernel(const float* __restrict__ A, const float* __restrict__ Bm, float
       const int64_t row = m0 + (it >> 2);
       const int kk = k0 + 4 * (it & 3);
       if constexpr (VEC) {
-        ra[u] = (row < M && kk < K) ? *reinterpret_cast<const float4*>(A + row * K + kk)
+        ra[u] = (row < M && kk < K) ? *reinterpret_cast<const float4*>(A + row * lda + kk)
                                     : make_float4(0.f, 0.f, 0.f, 0.f);
       } else {
-        const float* ar = A + (row < M ? row : 0) * K;
+        const float* ar = A + (row < M ? row : 0) * lda;
         ra[u].x = (row < M && kk < K) ? ar[kk] : 0.f;
         ra[u].y = (row < M && kk + 1 < K) ? ar[kk + 1] : 0.f;
         ra[u].z = (row < M && kk + 2 < K) ? ar[kk + 2] : 0.f;
@@ -407,27 +416,98 @@ gemm_rows_f32_kernel(const float* __restrict__ A, const float* __restrict__ Bm, 
   }
 }
 
+// Sum of the split-K partial products P[z] (z in order) with the GEMM's epilogue; N % 4 == 0.
+// C may be the residual (aux): each element reads it, then overwrites it, in one thread.
+template <int EPI>
+__global__ void __launch_bounds__(256) splitk_reduce_kernel(const float* __restrict__ P, float* C, const float* aux,
+                                                            int64_t M, int N, int S, int64_t cz, int h_rows,
+                                                            int64_t row0) {
+  const int64_t i4 = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
+  if (i4 >= M * N / 4) return;
+  float4 v = *reinterpret_cast<const float4*>(P + 4 * i4);
+  for (int z = 1; z < S; ++z) {
+    const float4 w = *reinterpret_cast<const float4*>(P + z * cz + 4 * i4);
+    v.x += w.x;
+    v.y += w.y;
+    v.z += w.z;
+    v.w += w.w;
+  }
+  const int64_t row = 4 * i4 / N;
+  const int col = static_cast<int>(4 * i4 - row * N);
+  if constexpr (EPI == kEpiCond) {
+    const float4 hv = *reinterpret_cast<const float4*>(aux + ((row0 + row) % h_rows) * N + col);
+    v.x *= hv.x;
+    v.y *= hv.y;
+    v.z *= hv.z;
+    v.w *= hv.w;
+  }
+  if constexpr (EPI == kEpiResidual) {
+    const float4 rv = *reinterpret_cast<const float4*>(aux + row * N + col);
+    v.x += rv.x;
+    v.y += rv.y;
+    v.z += rv.z;
+    v.w += rv.w;
+  }
+  if constexpr (EPI == kEpiRowMask) {
+    const float mk = reinterpret_cast<const uint8_t*>(aux)[row] != 0 ? 1.f : 0.f;
+    v.x *= mk;
+    v.y *= mk;
+    v.z *= mk;
+    v.w *= mk;
+  }
+  *reinterpret_cast<float4*>(C + 4 * i4) = v;
+}
+
 template <int EPI>
 hipError_t launch_gemm(const float* A, const float* B, float* C, const float* aux, int64_t M, int N, int K,
-                       int h_rows, int64_t row0, hipStream_t stream) {
+                       int h_rows, int64_t row0, hipStream_t stream, float* split_ws = nullptr,
+                       int64_t split_cap = 0) {
   const dim3 grid(static_cast<unsigned>((N + kBN - 1) / kBN), static_cast<unsigned>((M + kBM - 1) / kBM));
+  // Split K where the tiles leave most CUs idle (the tree's deep levels: 1024-4096 rows,
+  // 64-512 tiles of 96-step K chains): S parts of K into split_ws [S, M, N], then one pass
+  // that sums the parts in order and applies the epilogue (deterministic).
+  if (split_ws != nullptr && N % 4 == 0 && K % 4 == 0 && K >= 256) {
+    int cus = 0;
+    if (hipError_t err = device_cu_count(&cus); err != hipSuccess) return err;
+    const int64_t tiles = static_cast<int64_t>(grid.x) * grid.y;
+    const int64_t mn = M * N;
+    int64_t S = tiles < cus ? (2 * cus + tiles - 1) / tiles : 1;
+    S = S > 8 ? 8 : S;
+    S = S > K / 128 ? K / 128 : S;
+    S = S > split_cap / mn ? split_cap / mn : S;
+    if (S >= 2) {
+      const int kp = static_cast<int>(((K + S - 1) / S + kBK - 1) / kBK * kBK);
+      const int parts = (K + kp - 1) / kp;
+      const dim3 gs(grid.x, grid.y, static_cast<unsigned>(parts));
+      hipLaunchKernelGGL((gemm_f32_kernel<kEpiPlain, true>), gs, dim3(256), 0, stream, A, B, split_ws, nullptr, M, N,
+                         kp, 1, int64_t(0), K, K, mn);
+      if (hipError_t err = hipGetLastError(); err != hipSuccess) return err;
+      const int64_t n4 = mn / 4;
+      hipLaunchKernelGGL((splitk_reduce_kernel<EPI>), dim3(static_cast<unsigned>((n4 + 255) / 256)), dim3(256), 0,
+                         stream, split_ws, C, aux, M, N, parts, mn, h_rows, row0);
+      return hipGetLastError();
+    }
+  }
   if (N % 4 == 0 && K % 4 == 0)
-    hipLaunchKernelGGL((gemm_f32_kernel<EPI, true>), grid, dim3(256), 0, stream, A, B, C, aux, M, N, K, h_rows, row0);
+    hipLaunchKernelGGL((gemm_f32_kernel<EPI, true>), grid, dim3(256), 0, stream, A, B, C, aux, M, N, K, h_rows, row0,
+                       K, K, int64_t(0));
   else
     hipLaunchKernelGGL((gemm_f32_kernel<EPI, false>), grid, dim3(256), 0, stream, A, B, C, aux, M, N, K, h_rows,
-                       row0);
+                       row0, K, K, int64_t(0));
   return hipGetLastError();
 }
 
 // One factorized apply over rows [row0, row0 + M) of the caller's range: x, residual and y
-// point at row row0; work holds M x R floats.
+// point at row row0; work holds M x R floats; split_ws (split_cap floats, may be null) is free
+// scratch for split-K partial products.
 hipError_t apply_rows(const float* x, const float* V, const float* h, const float* U, const float* residual,
                       float* y, float* work, int64_t M, int d_in, int R, int d_out, int h_rows, int64_t row0,
-                      hipStream_t stream) {
-  hipError_t err = launch_gemm<kEpiCond>(x, V, work, h, M, R, d_in, h_rows, row0, stream);
+                      hipStream_t stream, float* split_ws = nullptr, int64_t split_cap = 0) {
+  hipError_t err = launch_gemm<kEpiCond>(x, V, work, h, M, R, d_in, h_rows, row0, stream, split_ws, split_cap);
   if (err != hipSuccess) return err;
-  if (residual != nullptr) return launch_gemm<kEpiResidual>(work, U, y, residual, M, d_out, R, 1, 0, stream);
-  return launch_gemm<kEpiPlain>(work, U, y, nullptr, M, d_out, R, 1, 0, stream);
+  if (residual != nullptr)
+    return launch_gemm<kEpiResidual>(work, U, y, residual, M, d_out, R, 1, 0, stream, split_ws, split_cap);
+  return launch_gemm<kEpiPlain>(work, U, y, nullptr, M, d_out, R, 1, 0, stream, split_ws, split_cap);
 }
 
 // Device addresses of the no-alloc workspace, one per device, resolved on first use.
@@ -570,6 +650,8 @@ hipError_t launch_compiled_wavefunction(const WaveFnParams& p, hipStream_t strea
   float *z = ws + L.z, *work = ws + L.work, *raw = ws + L.raw, *psi = ws + L.psi;
   float* u_buf[2] = {ws + L.u0, ws + L.u1};
   float* s_buf[2] = {ws + L.s0, ws + L.s1};
+  // the carrier buffer a step does not use holds its split-K partial products
+  const int64_t u_cap[2] = {L.u1 - L.u0, L.raw - L.u1};
   const int64_t rows = p.B * p.n;
   const int G = p.d_m / kQR;
   hipError_t err;
@@ -577,7 +659,7 @@ hipError_t launch_compiled_wavefunction(const WaveFnParams& p, hipStream_t strea
   if ((err = launch_gemm<kEpiPlain>(p.q, p.q_weight, z, nullptr, rows, p.d_z, p.d_q, 1, 0, stream)) != hipSuccess)
     return err;
   if ((err = apply_rows(z, p.leaf_V, p.leaf_h, p.leaf_U, nullptr, u_buf[0], work, rows, p.d_z, p.r_leaf, p.d_m, p.n, 0,
-                        stream)) != hipSuccess)
+                        stream, u_buf[1], u_cap[1])) != hipSuccess)
     return err;
   hipLaunchKernelGGL(normalize_rows_kernel, dim3(static_cast<unsigned>((rows + 3) / 4)), dim3(256), 0, stream,
                      u_buf[0], s_buf[0], rows, p.d_m);
@@ -594,7 +676,7 @@ hipError_t launch_compiled_wavefunction(const WaveFnParams& p, hipStream_t strea
       return err;
     // out = raw + ((raw V) o h_level[node]) U, written over raw
     if ((err = apply_rows(raw, p.merge_V, h_level, p.merge_U, raw, raw, work, m, p.d_m, p.r_merge, p.d_m, width, 0,
-                          stream)) != hipSuccess)
+                          stream, u_buf[cur ^ 1], u_cap[cur ^ 1])) != hipSuccess)
       return err;
     hipLaunchKernelGGL(level_gate_kernel, dim3(static_cast<unsigned>((m + 3) / 4)), dim3(256), 0, stream, raw, u_in,
                        s_buf[cur], ops, u_buf[cur ^ 1], s_buf[cur ^ 1], m, width, p.d_m, p.merge_eps);
@@ -603,7 +685,7 @@ hipError_t launch_compiled_wavefunction(const WaveFnParams& p, hipStream_t strea
   }
   // readout: psi = ((u_root V) o readout_h) U, then log|psi| and phase
   if ((err = apply_rows(u_buf[cur], p.readout_V, p.readout_h, p.readout_U, nullptr, psi, work, p.B, p.d_m, p.r_out, 2,
-                        1, 0, stream)) != hipSuccess)
+                        1, 0, stream, u_buf[cur ^ 1], u_cap[cur ^ 1])) != hipSuccess)
     return err;
   hipLaunchKernelGGL(readout_kernel, dim3(static_cast<unsigned>((p.B + 255) / 256)), dim3(256), 0, stream, psi,
                      s_buf[cur], p.log_abs, p.phase, p.B);
