@@ -215,11 +215,13 @@ def timed(step, steps, warmup, stream):
     return ev0.elapsed_time(ev1) / steps
 
 
-def algorithmic(work, B, N, H, D, n_phys, T, esize, with_e=False):
+def algorithmic(work, B, N, H, D, n_phys, T, esize, with_e=False, e_compact=False):
     """Algorithmic bytes and flops of one step.
 
     padded: every [B,N,H,D] tensor read or written once at the padded shape, plus the mask
-            (uint8) and, with a bias, e and its T tangents [B,N,H,N] read once; flops
+            (uint8) and, with a bias, e and its T tangents [B,N,H,N] read once (e_compact:
+            the compacted physical-pair layout holds only the physical pairs, so its bias
+            counts n_phys^2 entries per (walker, head) in both figures); flops
             (2 + 4T) G for fwd+JVP, 2G fwd, 6G fwd+VJP, G = 2 N^2 D per (walker, head),
             recompute not counted.
     effective: the same with the mask taken into account — inputs are needed only on
@@ -246,8 +248,8 @@ def algorithmic(work, B, N, H, D, n_phys, T, esize, with_e=False):
     else:
         raise ValueError(work)
     n_e_out = 1 if work in ("fwd_vjp", "fwd_vjp_gated") else 0  # de (every pair) when the bias is an input
-    e_pad = (n_e + n_e_out) * N * H * N * esize if with_e else 0
     e_eff = (n_e * n_phys * n_phys + n_e_out * N * N) * H * esize if with_e else 0
+    e_pad = e_eff if e_compact else ((n_e + n_e_out) * N * H * N * esize if with_e else 0)
     padded_bytes = int(B * (N * rowb * (n_in + n_out) + N + lse_b + e_pad))
     eff_bytes = int(B * (n_phys * rowb * n_in + N * rowb * n_out + N + lse_b + e_eff))
     padded_flops = B * H * g_mult * 2 * N * N * D
@@ -379,7 +381,8 @@ def run_attention(args, cfg):
     # physical rows only) are below twice the 256 MB Infinity Cache run on enough copies of
     # their buffers, used in turn, that no step finds its inputs left in the cache by the
     # previous steps. --buffer-sets overrides the count (1: every step on the same buffers).
-    alg = algorithmic(cfg.work, B, N, H, D, cfg.n_phys, T, esize, cfg.with_e)
+    alg = algorithmic(cfg.work, B, N, H, D, cfg.n_phys, T, esize, cfg.with_e,
+                      e_compact=cfg.with_e and cfg.e_layout == "compact")
     copies = max(1, -(-2 * INFINITY_CACHE_BYTES // alg["eff_bytes"]))
     if args.buffer_sets:
         copies = args.buffer_sets

@@ -46,6 +46,18 @@ constexpr int kSlotBytes = 144;  // int16 perm[64], int32 n_phys at byte 128
 constexpr int kRoleBytes = 132;  // slot 0: one byte per wave for the role exchange (below)
 constexpr int kDmaBytes = 1024;  // bytes one 16-byte-per-lane wave instruction moves
 
+// D = 32 forward+tangent: the two 16-row tiles of O^T (and A^T, C^T) cover the features
+// d = 2 i + dt (i = tile row, dt = tile) instead of 16 dt + i, so a lane's two V values of a
+// contraction step (features 2 c, 2 c + 1) are one 8-byte LDS read instead of two 4-byte
+// reads, and a lane's eight outputs are the contiguous features 8 g .. 8 g + 7. (While the
+// partner wave's products run, an LDS read instruction costs a wave ~80 cycles whatever its
+// width: c2 89.5 -> 88.7 us, the gated c2 shape 89.3 -> 88.0 us on MI355X; the forward-only
+// and tangent-only kernels of the two-launch route measured 0.7% slower and keep 4-byte reads.)
+template <int D, int T, bool GIVEN_LSE>
+constexpr bool pc_pair_d() {
+  return D == 32 && T > 0 && !GIVEN_LSE;
+}
+
 template <int D, int T>
 struct PcShape {
   static constexpr int NT = 2 + 2 * T;  // K, Kt[T], V, Vt[T]
@@ -69,6 +81,11 @@ struct PcShape {
 // Row staging of the bias (mode 2 below): a consumer wave loads its 16 query rows whole and
 // gathers its keys from them through LDS, one region per tensor (e, e_t[t]). Row cq of a
 // region sits at cq * kERowF floats (64 keys and a pad that keeps rows 16-byte aligned).
+// Rows of the compacted layout hold the keys in the item's key order, so they are staged
+// with the keys of every 16-key block permuted (key 16 q + 4 r + u at 16 q + 4 u + r): a
+// lane's four keys of a key tile are then one 16-byte read instead of four 4-byte reads.
+// While the partner wave's products run, an LDS read instruction costs a wave ~80 cycles
+// whatever its width (MI355X), so this takes the gated trunk call from 286 to 244 us.
 // Served where two workgroups per CU still fit (D = 8; D = 16 with T <= 1; D = 32 with
 // T = 0); sharing one region between the tensors costs more than it saves (measured at
 // D = 32, T = 1: 139 against 137 us).
@@ -491,6 +508,7 @@ __device__ __forceinline__ void pc_tile(const FwdParams& p, const char* buf, con
   const int jq = tile * 16 + c;
   const bool qvalid = jq < nq;
   const int qsite = qs.qsite;
+  constexpr bool kPairD = pc_pair_d<D, T, GIVEN_LSE>();
 
   // ---- bias (and its tangents) for this lane's 4 NJ scores: issued first -------------
   float ev[NJ][4];
@@ -633,11 +651,26 @@ __device__ __forceinline__ void pc_tile(const FwdParams& p, const char* buf, con
   // ---- row-staged bias: the rows go to LDS while the matrix cores work on S -----------
   constexpr int kRF = PcEStage<D, T>::kERowF;
   if constexpr (ROWS) {
+    if (cmp) {
+      // compacted rows: key 16 q + 4 r + u of a staged row at 16 q + 4 u + r, so a lane's
+      // four keys of one key tile (4 r + g, r = 0..3) are one 16-byte read below
 #pragma unroll
-    for (int x = 0; x <= T; ++x)
+      for (int x = 0; x <= T; ++x)
 #pragma unroll
-      for (int i = 0; i < 4; ++i)
-        *reinterpret_cast<float4*>(estage + (x * 16 + 4 * i + g) * kRF + 4 * c) = erow[x][i];
+        for (int i = 0; i < 4; ++i) {
+          float* const w = estage + (x * 16 + 4 * i + g) * kRF + 16 * (c >> 2) + (c & 3);
+          w[0] = erow[x][i].x;
+          w[4] = erow[x][i].y;
+          w[8] = erow[x][i].z;
+          w[12] = erow[x][i].w;
+        }
+    } else {
+#pragma unroll
+      for (int x = 0; x <= T; ++x)
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+          *reinterpret_cast<float4*>(estage + (x * 16 + 4 * i + g) * kRF + 4 * c) = erow[x][i];
+    }
   }
 
   // ---- V and Vt rows for the products, read while the matrix cores finish S -----------
@@ -645,6 +678,23 @@ __device__ __forceinline__ void pc_tile(const FwdParams& p, const char* buf, con
   const int vcol = (D % 16 == 0) ? c : min(c, D - 1);
   float va[NJ][4][DT];
   float vta[NJ][TT][4][DT];
+  if constexpr (kPairD) {
+#pragma unroll
+    for (int jt = 0; jt < NJ; ++jt)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int off = swz_off<D>(jt * 16 + 4 * r + g, c >> 1) + (c & 1) * 8;
+        const float2 x = *reinterpret_cast<const float2*>(V0 + off);
+        va[jt][r][0] = x.x;
+        va[jt][r][1] = x.y;
+#pragma unroll
+        for (int t = 0; t < T; ++t) {
+          const float2 y = *reinterpret_cast<const float2*>(V0 + (1 + t) * Sh::TILE + off);
+          vta[jt][t][r][0] = y.x;
+          vta[jt][t][r][1] = y.y;
+        }
+      }
+  } else {
 #pragma unroll
   for (int jt = 0; jt < NJ; ++jt)
 #pragma unroll
@@ -657,26 +707,46 @@ __device__ __forceinline__ void pc_tile(const FwdParams& p, const char* buf, con
 #pragma unroll
         for (int t = 0; t < T; ++t) vta[jt][t][r][dt] = *reinterpret_cast<const float*>(V0 + (1 + t) * Sh::TILE + off);
       }
+  }
   compiler_fence();
 
   // ---- row-staged bias: this lane's keys from the staged rows (the wave reads only what
   // it wrote, and its LDS accesses complete in order) ----------------------------------
   if constexpr (ROWS) {
+    if (cmp) {
 #pragma unroll
-    for (int x = 0; x <= T; ++x) {
-      const float* const rg = estage + x * 16 * kRF;
+      for (int x = 0; x <= T; ++x) {
+        const float* const rg = estage + x * 16 * kRF + c * kRF + 4 * g;
 #pragma unroll
-      for (int jt = 0; jt < NJ; ++jt)
+        for (int jt = 0; jt < NJ; ++jt) {
+          const float4 v = *reinterpret_cast<const float4*>(rg + 16 * jt);
+          const float vr[4] = {v.x, v.y, v.z, v.w};
 #pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          const int j = jt * 16 + 4 * r + g;
-          const int ks = (key_all || cmp) ? j : static_cast<int>(slot_perm[j & 63]);
-          const float val = rg[c * kRF + ks];
-          if (x == 0)
-            ev[jt][r] = val;
-          else
-            etv[x - 1][jt][r] = val;
+          for (int r = 0; r < 4; ++r) {
+            if (x == 0)
+              ev[jt][r] = vr[r];
+            else
+              etv[x - 1][jt][r] = vr[r];
+          }
         }
+      }
+    } else {
+#pragma unroll
+      for (int x = 0; x <= T; ++x) {
+        const float* const rg = estage + x * 16 * kRF;
+#pragma unroll
+        for (int jt = 0; jt < NJ; ++jt)
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            const int j = jt * 16 + 4 * r + g;
+            const int ks = key_all ? j : static_cast<int>(slot_perm[j & 63]);
+            const float val = rg[c * kRF + ks];
+            if (x == 0)
+              ev[jt][r] = val;
+            else
+              etv[x - 1][jt][r] = val;
+          }
+      }
     }
   }
 
@@ -777,6 +847,11 @@ __device__ __forceinline__ void pc_tile(const FwdParams& p, const char* buf, con
 #pragma unroll
     for (int r = 0; r < 4; ++r) ov[dt][r] = GIVEN_LSE ? qs.oin[dt][r] : o[dt][r] * inv;
   sq();
+  // Store u (u < DT) writes features sd0(u) .. sd0(u) + 3; its m-th value is element
+  // (sdt(u, m), sr(u, m)) of a lane's [DT][4] outputs.
+  auto sd0 = [&](int u) { return kPairD ? 8 * g + 4 * u : u * 16 + 4 * g; };
+  auto sdt = [&](int u, int m) { return kPairD ? (m & 1) : u; };
+  auto sr = [&](int u, int m) { return kPairD ? 2 * u + (m >> 1) : m; };
 
   // ---- stores: unconditional, invalid lanes past the walker's last record ------------
   if constexpr (ROLE == 1) {
@@ -797,27 +872,31 @@ __device__ __forceinline__ void pc_tile(const FwdParams& p, const char* buf, con
     const int64_t ywrow = static_cast<int64_t>(N) * hh * D;  // floats of y per walker
     const int ybytes = static_cast<int>(ywrow * 4);
     const int ybase = (qsite * hh + (h - hh)) * D;
-    auto yoff = [&](int dt) {
-      const int d0 = dt * 16 + 4 * g;
+    auto yoff = [&](int u) {
+      const int d0 = sd0(u);
       return (qvalid && (D % 16 == 0 || d0 < D)) ? (ybase + d0) * 4 : ybytes;
     };
     const __amdgpu_buffer_rsrc_t y_rs = make_rsrc(static_cast<float*>(p.out) + b * ywrow, ybytes);
 #pragma unroll
-    for (int dt = 0; dt < DT; ++dt)
-      buf_store4(y_rs, yoff(dt), gr.s[dt][0] * ov[dt][0], gr.s[dt][1] * ov[dt][1], gr.s[dt][2] * ov[dt][2],
-                 gr.s[dt][3] * ov[dt][3]);
+    for (int u = 0; u < DT; ++u) {
+      float yv[4];
+#pragma unroll
+      for (int m = 0; m < 4; ++m) yv[m] = gr.s[sdt(u, m)][sr(u, m)] * ov[sdt(u, m)][sr(u, m)];
+      buf_store4(y_rs, yoff(u), yv[0], yv[1], yv[2], yv[3]);
+    }
 #pragma unroll
     for (int t = 0; t < T; ++t) {
       const __amdgpu_buffer_rsrc_t t_rs = make_rsrc(static_cast<float*>(p.tout) + t * p.y_tstride + b * ywrow, ybytes);
 #pragma unroll
-      for (int dt = 0; dt < DT; ++dt) {
+      for (int u = 0; u < DT; ++u) {
         float tv[4];
 #pragma unroll
-        for (int r = 0; r < 4; ++r) {
+        for (int m = 0; m < 4; ++m) {
+          const int dt = sdt(u, m), r = sr(u, m);
           const float od = fmaf(-mut[t], ov[dt][r], fmaf(at[t][dt][r], inv_ln2, ct[t][dt][r] * inv));
-          tv[r] = fmaf(gr.d[t][dt][r], ov[dt][r], gr.s[dt][r] * od);
+          tv[m] = fmaf(gr.d[t][dt][r], ov[dt][r], gr.s[dt][r] * od);
         }
-        buf_store4(t_rs, yoff(dt), tv[0], tv[1], tv[2], tv[3]);
+        buf_store4(t_rs, yoff(u), tv[0], tv[1], tv[2], tv[3]);
       }
     }
     return;
@@ -828,10 +907,11 @@ __device__ __forceinline__ void pc_tile(const FwdParams& p, const char* buf, con
   if constexpr (!GIVEN_LSE) {
     const __amdgpu_buffer_rsrc_t o_rs = make_rsrc(static_cast<float*>(p.out) + b * wrow, obytes);
 #pragma unroll
-    for (int dt = 0; dt < DT; ++dt) {
-      const int d0 = dt * 16 + 4 * g;
+    for (int u = 0; u < DT; ++u) {
+      const int d0 = sd0(u);
       const int voff = (qvalid && (D % 16 == 0 || d0 < D)) ? (obase + d0) * 4 : obytes;
-      buf_store4(o_rs, voff, ov[dt][0], ov[dt][1], ov[dt][2], ov[dt][3]);
+      buf_store4(o_rs, voff, ov[sdt(u, 0)][sr(u, 0)], ov[sdt(u, 1)][sr(u, 1)], ov[sdt(u, 2)][sr(u, 2)],
+                 ov[sdt(u, 3)][sr(u, 3)]);
     }
     const int lbytes = N * H * 4;
     const __amdgpu_buffer_rsrc_t l_rs =
@@ -843,12 +923,15 @@ __device__ __forceinline__ void pc_tile(const FwdParams& p, const char* buf, con
   for (int t = 0; t < T; ++t) {
     const __amdgpu_buffer_rsrc_t t_rs = make_rsrc(static_cast<float*>(p.tout) + t * p.t_stride + b * wrow, obytes);
 #pragma unroll
-    for (int dt = 0; dt < DT; ++dt) {
-      const int d0 = dt * 16 + 4 * g;
+    for (int u = 0; u < DT; ++u) {
+      const int d0 = sd0(u);
       const int voff = (qvalid && (D % 16 == 0 || d0 < D)) ? (obase + d0) * 4 : obytes;
       float tv[4];
 #pragma unroll
-      for (int r = 0; r < 4; ++r) tv[r] = fmaf(-mut[t], ov[dt][r], fmaf(at[t][dt][r], inv_ln2, ct[t][dt][r] * inv));
+      for (int m = 0; m < 4; ++m) {
+        const int dt = sdt(u, m), r = sr(u, m);
+        tv[m] = fmaf(-mut[t], ov[dt][r], fmaf(at[t][dt][r], inv_ln2, ct[t][dt][r] * inv));
+      }
       buf_store4(t_rs, voff, tv[0], tv[1], tv[2], tv[3]);
     }
   }
