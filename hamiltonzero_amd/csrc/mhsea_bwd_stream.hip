@@ -30,6 +30,33 @@
 namespace hz {
 namespace {
 
+// D = 32: the two tiles of dq^T, dk^T, dv^T cover the even and odd features (d = 2 i + dt,
+// i = tile row, dt = tile) instead of the low and high halves, so a lane's two values of a
+// transposed operand (K in phase A, dout and q in phase B; features 2 c, 2 c + 1) are one
+// 8-byte LDS read instead of two 4-byte reads, and a lane's eight results are the contiguous
+// features 8 g .. 8 g + 7. While the partner wave's products run, an LDS read instruction
+// costs a wave ~80 cycles whatever its width (MI355X): c2vjp 178.0 -> 161.2 us, c2e_vjp
+// 245.5 -> 238.0 us. Four features per lane at D = 64 (one 16-byte read) made c3f32 24%
+// slower (the one-wave-per-SIMD instantiation) and is not used.
+template <int D>
+constexpr bool bwd_pack_d() {
+  return D == 32;
+}
+template <int DT>
+__device__ __forceinline__ void lds_frag(const float* p, float (&x)[DT]) {
+  if constexpr (DT == 4) {
+    const float4 v = *reinterpret_cast<const float4*>(p);
+    x[0] = v.x;
+    x[1] = v.y;
+    x[2] = v.z;
+    x[3] = v.w;
+  } else {
+    const float2 v = *reinterpret_cast<const float2*>(p);
+    x[0] = v.x;
+    x[1] = v.y;
+  }
+}
+
 template <int D>
 struct BwdStreamShape {
   static constexpr int KC = 64;
@@ -229,6 +256,13 @@ __global__ void __launch_bounds__(256, ((ROWS && D == 32) ? 2 : BwdStreamShape<D
     const int nqt = (nq + 15) >> 4, nkt = (nk + 15) >> 4;
     const int64_t e_walker = static_cast<int64_t>(bc) * N * N * H + static_cast<int64_t>(hc) * p.e_sh;
 
+    // store u of a lane's [DT][4] results writes features sd0(u) .. sd0(u) + 3, its m-th
+    // value being element (sdt(u, m), sr(u, m))
+    constexpr bool kPack = bwd_pack_d<D>();
+    auto sd0 = [&](int u) { return kPack ? 4 * DT * g + 4 * u : u * 16 + 4 * g; };
+    auto sdt = [&](int u, int m) { return kPack ? (4 * u + m) % DT : u; };
+    auto sr = [&](int u, int m) { return kPack ? (4 * u + m) / DT : m; };
+
     // ---- phase A: dq (and de), wave = 16 queries ----------------------------------------
     if (wave < nqt) {
       const int jq = wave * 16 + c;
@@ -286,6 +320,15 @@ __global__ void __launch_bounds__(256, ((ROWS && D == 32) ? 2 : BwdStreamShape<D
               }
             }
           }
+          if constexpr (bwd_pack_d<D>()) {
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+              float ka[DT];
+              lds_frag<DT>(Ks + (jt * 16 + 4 * g + r) * LD + DT * c, ka);
+#pragma unroll
+              for (int dt = 0; dt < DT; ++dt) dqa[dt] = mfma16x4(ka[dt], dsv[r], dqa[dt]);
+            }
+          } else {
 #pragma unroll
           for (int dt = 0; dt < DT; ++dt) {
             const int col = dt * 16 + c;
@@ -295,17 +338,18 @@ __global__ void __launch_bounds__(256, ((ROWS && D == 32) ? 2 : BwdStreamShape<D
               dqa[dt] = mfma16x4(ka, dsv[r], dqa[dt]);
             }
           }
+          }
         }
         __builtin_amdgcn_sched_barrier(0);
       }
       if (qvalid) {
         const int64_t obase = bnhd(bc, qsite, hc, N, H, D);
 #pragma unroll
-        for (int dt = 0; dt < DT; ++dt) {
-          const int d0 = dt * 16 + 4 * g;
+        for (int u = 0; u < DT; ++u) {
+          const int d0 = sd0(u);
           if (D % 16 != 0 && d0 >= D) continue;
-          store4<S>(p.dq, obase + d0, dqa[dt][0] * p.scale, dqa[dt][1] * p.scale,
-                    dqa[dt][2] * p.scale, dqa[dt][3] * p.scale);
+          store4<S>(p.dq, obase + d0, dqa[sdt(u, 0)][sr(u, 0)] * p.scale, dqa[sdt(u, 1)][sr(u, 1)] * p.scale,
+                    dqa[sdt(u, 2)][sr(u, 2)] * p.scale, dqa[sdt(u, 3)][sr(u, 3)] * p.scale);
         }
       }
     }
@@ -339,6 +383,22 @@ __global__ void __launch_bounds__(256, ((ROWS && D == 32) ? 2 : BwdStreamShape<D
             dp = mfma16x4(grow[s], vf[s], dp);
           }
           float pv[4], dsv[4];
+          // the four rows' lse and delta read ahead of the row loop: one 16-byte read each at
+          // D = 32, 4-byte reads at D = 64 (c3f32 1768 -> 1692 us); D <= 16 reads them inside
+          // the loop (hoisted, the gated trunk's reverse mode measured 692 -> 737 us)
+          float l2r[4], dlr[4];
+          if constexpr (D == 32) {
+            const float4 l2v = *reinterpret_cast<const float4*>(L2s + it * 16 + 4 * g);
+            const float4 dlv = *reinterpret_cast<const float4*>(Dls + it * 16 + 4 * g);
+            l2r[0] = l2v.x, l2r[1] = l2v.y, l2r[2] = l2v.z, l2r[3] = l2v.w;
+            dlr[0] = dlv.x, dlr[1] = dlv.y, dlr[2] = dlv.z, dlr[3] = dlv.w;
+          } else if constexpr (D == 64) {
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+              l2r[r] = L2s[it * 16 + 4 * g + r];
+              dlr[r] = Dls[it * 16 + 4 * g + r];
+            }
+          }
 #pragma unroll
           for (int r = 0; r < 4; ++r) {
             const int il = it * 16 + 4 * g + r;
@@ -354,9 +414,23 @@ __global__ void __launch_bounds__(256, ((ROWS && D == 32) ? 2 : BwdStreamShape<D
                                           static_cast<int64_t>(ksite) * p.e_sk);
               }
             }
-            pv[r] = valid ? lse_weight(sv * kLog2e - L2s[il]) : 0.f;
-            dsv[r] = pv[r] * (dp[r] - Dls[il]);
+            pv[r] = valid ? lse_weight(sv * kLog2e - (D >= 32 ? l2r[r] : L2s[il])) : 0.f;
+            dsv[r] = pv[r] * (dp[r] - (D >= 32 ? dlr[r] : Dls[il]));
           }
+          if constexpr (bwd_pack_d<D>()) {
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+              const int row = it * 16 + 4 * g + r;
+              float ga[DT], qa[DT];
+              lds_frag<DT>(Gs + row * LD + DT * c, ga);
+              lds_frag<DT>(Qs + row * LD + DT * c, qa);
+#pragma unroll
+              for (int dt = 0; dt < DT; ++dt) {
+                dva[dt] = mfma16x4(ga[dt], pv[r], dva[dt]);
+                dka[dt] = mfma16x4(qa[dt], dsv[r], dka[dt]);
+              }
+            }
+          } else {
 #pragma unroll
           for (int dt = 0; dt < DT; ++dt) {
             const int col = dt * 16 + c;
@@ -370,17 +444,20 @@ __global__ void __launch_bounds__(256, ((ROWS && D == 32) ? 2 : BwdStreamShape<D
               dka[dt] = mfma16x4(qa, dsv[r], dka[dt]);
             }
           }
+          }
         }
         __builtin_amdgcn_sched_barrier(0);
       }
       if (kvalid) {
         const int64_t obase = bnhd(bc, ksite, hc, N, H, D);
 #pragma unroll
-        for (int dt = 0; dt < DT; ++dt) {
-          const int d0 = dt * 16 + 4 * g;
+        for (int u = 0; u < DT; ++u) {
+          const int d0 = sd0(u);
           if (D % 16 != 0 && d0 >= D) continue;
-          store4<S>(p.dk, obase + d0, dka[dt][0], dka[dt][1], dka[dt][2], dka[dt][3]);
-          store4<S>(p.dv, obase + d0, dva[dt][0], dva[dt][1], dva[dt][2], dva[dt][3]);
+          store4<S>(p.dk, obase + d0, dka[sdt(u, 0)][sr(u, 0)], dka[sdt(u, 1)][sr(u, 1)], dka[sdt(u, 2)][sr(u, 2)],
+                    dka[sdt(u, 3)][sr(u, 3)]);
+          store4<S>(p.dv, obase + d0, dva[sdt(u, 0)][sr(u, 0)], dva[sdt(u, 1)][sr(u, 1)], dva[sdt(u, 2)][sr(u, 2)],
+                    dva[sdt(u, 3)][sr(u, 3)]);
         }
       }
     }
