@@ -46,16 +46,17 @@ constexpr int kSlotBytes = 144;  // int16 perm[64], int32 n_phys at byte 128
 constexpr int kRoleBytes = 132;  // slot 0: one byte per wave for the role exchange (below)
 constexpr int kDmaBytes = 1024;  // bytes one 16-byte-per-lane wave instruction moves
 
-// D = 32 forward+tangent: the two 16-row tiles of O^T (and A^T, C^T) cover the features
-// d = 2 i + dt (i = tile row, dt = tile) instead of 16 dt + i, so a lane's two V values of a
-// contraction step (features 2 c, 2 c + 1) are one 8-byte LDS read instead of two 4-byte
-// reads, and a lane's eight outputs are the contiguous features 8 g .. 8 g + 7. (While the
-// partner wave's products run, an LDS read instruction costs a wave ~80 cycles whatever its
-// width: c2 89.5 -> 88.7 us, the gated c2 shape 89.3 -> 88.0 us on MI355X; the forward-only
-// and tangent-only kernels of the two-launch route measured 0.7% slower and keep 4-byte reads.)
+// D = 32 (not the tangent-only kernel): the two 16-row tiles of O^T (and A^T, C^T) cover the
+// features d = 2 i + dt (i = tile row, dt = tile) instead of 16 dt + i, so a lane's two V
+// values of a contraction step (features 2 c, 2 c + 1) are one 8-byte LDS read instead of two
+// 4-byte reads, and a lane's eight outputs are the contiguous features 8 g .. 8 g + 7. (While
+// the partner wave's products run, an LDS read instruction costs a wave ~80 cycles whatever
+// its width: c2 89.5 -> 88.7 us, the gated c2 shape 89.3 -> 88.0 us, the forward-only kernel
+// of the two-launch route 0.4% faster on MI355X; the tangent-only kernel, whose given out
+// rows then load as eight floats, measured 1% slower and keeps 4-byte reads.)
 template <int D, int T, bool GIVEN_LSE>
 constexpr bool pc_pair_d() {
-  return D == 32 && T > 0 && !GIVEN_LSE;
+  return D == 32 && !GIVEN_LSE;
 }
 
 template <int D, int T>
