@@ -305,23 +305,30 @@ __global__ void __launch_bounds__(256, ((D == 64 && T > 0) || (D == 32 && T == 2
 #pragma unroll
         for (int r = 0; r < 4; ++r) sc[jt][r] = lse_weight(sc[jt][r] - lse2);
     } else {
-      const float mnew = fmaxf(m2, group_max(mx));
-      if (MULTI && kc > 0) {
-        const float alpha = fast_exp2(m2 - mnew);
-        lsum *= alpha;
+      // Lazy rescale: a row's base m2 only moves when the chunk maximum exceeds it by more
+      // than 8 (base 2), so most chunks skip the rescale of the 4 DT (1 + 2 T) accumulators
+      // (weights stay below 2^8; the first chunk sets m2, which starts at -inf).
+      const float cmax = group_max(mx);
+      const bool need = cmax > m2 + 8.f;
+      if (__any(need)) {  // wave-uniform
+        const float mnew = need ? cmax : m2;
+        if (MULTI && kc > 0) {
+          const float alpha = fast_exp2(m2 - mnew);
+          lsum *= alpha;
 #pragma unroll
-        for (int dt = 0; dt < DT; ++dt) {
-          o[dt] *= alpha;
+          for (int dt = 0; dt < DT; ++dt) {
+            o[dt] *= alpha;
 #pragma unroll
-          for (int t = 0; t < T; ++t) {
-            at[t][dt] *= alpha;
-            ct[t][dt] *= alpha;
+            for (int t = 0; t < T; ++t) {
+              at[t][dt] *= alpha;
+              ct[t][dt] *= alpha;
+            }
           }
-        }
 #pragma unroll
-        for (int t = 0; t < T; ++t) mu[t] *= alpha;
+          for (int t = 0; t < T; ++t) mu[t] *= alpha;
+        }
+        m2 = mnew;
       }
-      m2 = mnew;
 #pragma unroll
       for (int jt = 0; jt < NJT; ++jt)
 #pragma unroll

@@ -371,12 +371,19 @@ __global__ void __launch_bounds__(64 * QT * HG) rect_attention_fwd_kernel(const 
         mx = fmaxf(mx, sc[jt][r]);
       }
     }
-    const float mnew = fmaxf(m2, group_max(mx));
-    const float alpha = fast_exp2(m2 - mnew);  // 0 on the first chunk (m2 = -inf)
-    lsum *= alpha;
+    // Lazy rescale: the base m2 only moves when the chunk maximum exceeds it by more than 8
+    // (base 2), so most chunks skip the rescale (weights stay below 2^8; the first chunk sets
+    // m2, which starts at -inf, and alpha is then 0)
+    const float cmax = group_max(mx);
+    const bool need = cmax > m2 + 8.f;
+    if (__any(need)) {  // wave-uniform
+      const float mnew = need ? cmax : m2;
+      const float alpha = fast_exp2(m2 - mnew);
+      lsum *= alpha;
 #pragma unroll
-    for (int dt = 0; dt < DT; ++dt) o[dt] *= alpha;
-    m2 = mnew;
+      for (int dt = 0; dt < DT; ++dt) o[dt] *= alpha;
+      m2 = mnew;
+    }
 #pragma unroll
     for (int jt = 0; jt < NJT; ++jt)
 #pragma unroll
