@@ -461,12 +461,24 @@ __global__ void __launch_bounds__(kThreads, 1) mhsea_fwd_bf16_ws_kernel(const Fw
       stage_loads(2 * kKC, 0, rk, rv);
       __syncthreads();
       for (int i = 0; i < nc; ++i) {
+        // site ids of this iteration's staging rows, read ahead of the products so their LDS
+        // latency hides under them
+        const int jk = (i + 3) * kKC + srow, jv = (i + 1) * kKC + srow;
+        int sk = idx[min(jk, N - 1)];
+        int sv = idx[min(jv, N - 1)];
         if (i > 0) pv_step(i - 1);
         // K(i+2) into K buffer (i+2) mod 3 (last read: K(i-1), in iteration i-1), V(i) into
         // V buffer i mod 2 (last read: V(i-2), in iteration i-1), then the next reads
         kstore((i + 2) % 3, rk);
         vstore(i & 1, rv);
-        stage_loads((i + 3) * kKC, (i + 1) * kKC, rk, rv);
+        asm volatile("" : "+v"(sk), "+v"(sv));
+        const int ko = jk < nk ? sk * rowstride + hoff + scol * 16 : wbytes;
+        const int vo = jv < nk ? sv * rowstride + hoff + scol * 16 : wbytes;
+#pragma unroll
+        for (int x = 0; x < NX; ++x) {
+          rk[x] = bload(kr[x], ko);
+          rv[x] = bload(vr[x], vo);
+        }
         __syncthreads();
       }
       pv_step(nc - 1);
