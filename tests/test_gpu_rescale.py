@@ -6,11 +6,11 @@ by about RISE (natural units) from the first key to the last: q and every key ro
 unit direction u, with key j's component along u growing linearly in j. Keys are visited in
 site order, so every chunked kernel has to move its base (and rescale its sums and
 accumulators) several times after the first chunk. Checked against the float64 oracle for
-each chunked forward family: the float32 LDS-streaming kernel (fp32, N > 64), the bfloat16
-kernels (64-key chunks, with a bias and at D = 32; 32-query tiles at D = 64 without one;
-N <= 128), the tangent directions, and the rectangular kernel with and without the head
-collapse. A base that is moved wrongly (a sum or an accumulator not rescaled, or rescaled by
-the wrong factor) gives errors of order one.
+each chunked forward family: the float32 LDS-streaming kernel (fp32, N > 64) and its gated
+variant (the trunk's head collapse), the bfloat16 kernels (64-key chunks, with a bias and at
+D = 32; 32-query tiles at D = 64 without one; N <= 128), the tangent directions, and the
+rectangular kernel with and without the head collapse. A base that is moved wrongly (a sum
+or an accumulator not rescaled, or rescaled by the wrong factor) gives errors of order one.
 
 Tolerances. Scores of magnitude RISE carry RISE times the absolute rounding of scores of order
 one, so float32 outputs are held to F32_TOL_RISING = 5e-5 here instead of 1e-5; bfloat16 ones
@@ -114,6 +114,39 @@ def test_rising_logits_fwd_jvp(case):
         ett = None if a["et"] is None else a["et"][t]
         ref_t = O.jvp(a["q"], a["k"], a["e"], a["v"], mask, a["qt"][t], a["kt"][t], ett, a["vt"][t])
         assert rel(_host(tout)[t], ref_t) <= tol, f"tangent {t}"
+
+
+# name, B, N, H, D, n_phys, bias, T
+GATED_CASES = [
+    ("gated_n256_d64_t2_bias", 2, 256, 4, 64, 230, True, 2),
+    ("gated_n200_d16_t1", 3, 200, 2, 16, 180, False, 1),
+]
+
+
+@pytest.mark.parametrize("case", GATED_CASES, ids=[c[0] for c in GATED_CASES])
+def test_rising_logits_gated(case):
+    """The head-collapse forward (fp32, N > 64: the LDS-streaming kernel's gated variant)."""
+    from hamiltonzero_amd import kernels
+
+    name, B, N, H, D, n_phys, with_e, T = case
+    _say(f"rising logits {name}")
+    q, k, v, u, rng = rising(zlib.crc32(name.encode()) % 1000, B, N, N, H, D)
+    mask = np.zeros((B, N), dtype=bool)
+    for b in range(B):
+        mask[b, np.sort(rng.permutation(N)[:n_phys])] = True
+    e = rng.standard_normal((B, N, H, N), dtype=np.float32) * np.float32(0.5) if with_e else None
+    qt, kt, vt = (rng.standard_normal((T, B, N, H, D), dtype=np.float32) for _ in range(3))
+    qt -= (qt @ u.astype(np.float32))[..., None] * u.astype(np.float32)  # qt . u = 0
+    et = rng.standard_normal((T, B, N, H, N), dtype=np.float32) if with_e else None
+    f = lambda x: _dev(x, torch.float32)
+    y, ty = kernels.mhsea_fwd_jvp_gated(f(q), f(k), f(v), _dev(mask, None), f(qt), f(kt), f(vt), f(e), f(et))
+    torch.cuda.synchronize()
+    for t in range(T):
+        ett = None if et is None else et[t]
+        ref_y, ref_ty = O.gated_fwd_jvp(q, k, e, v, mask, qt[t], kt[t], ett, vt[t])
+        if t == 0:
+            assert rel(_host(y), ref_y) <= F32_TOL_RISING
+        assert rel(_host(ty)[t], ref_ty) <= F32_TOL_RISING, f"tangent {t}"
 
 
 # B, Nq, Nk, H, D, n_phys (None: no mask), gated
