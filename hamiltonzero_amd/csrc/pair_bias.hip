@@ -406,10 +406,8 @@ hipError_t launch_pb_c(const PairBiasParams& p, int H, bool tan, int64_t blocks,
 }  // namespace
 
 hipError_t launch_pair_bias(PairBiasParams p, int C, int H, bool tan, hipStream_t stream) {
-  int device = 0, cus = 256;
-  if (hipGetDevice(&device) != hipSuccess ||
-      hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, device) != hipSuccess || cus < 1)
-    cus = 256;
+  int cus = 0;
+  if (hipError_t err = device_cu_count(&cus); err != hipSuccess) return err;
   const int64_t waves = static_cast<int64_t>(cus) * 2 * kPBWaves;
   // Parts per walker: about four items per wave, each part at least four tiles.
   const int64_t tp = tan ? 16 : 32;
