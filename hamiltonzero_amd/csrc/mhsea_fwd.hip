@@ -352,8 +352,12 @@ __global__ void __launch_bounds__(256, ((D == 64 && T > 0) || (D == 32 && T == 2
 #pragma unroll
     for (int jt = 0; jt < NJT; ++jt) {
       if (jt < njt) {
+        // contraction step r takes keys r, r + 4, r + 8, r + 12 of the tile: in a partial
+        // last tile the steps from its key count on hold padding only (weight 0) and are skipped
+        const int jrem = jn - jt * 16;  // wave-uniform
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
+          if (r > 0 && r >= jrem) break;
           const int row = jt * 16 + 4 * g + r;
           float va[DT], vta[TT][DT];
 #pragma unroll
