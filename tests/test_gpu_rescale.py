@@ -11,6 +11,13 @@ variant (the trunk's head collapse), the bfloat16 kernels (64-key chunks, with a
 D = 32; 32-query tiles at D = 64 without one; N <= 128), the tangent directions, and the
 rectangular kernel with and without the head collapse. A base that is moved wrongly (a sum
 or an accumulator not rescaled, or rescaled by the wrong factor) gives errors of order one.
+The reverse-mode kernels, which rebuild the weights from the stored lse, are run on the same
+inputs: dk, dv and de (dS itself) against the float64 oracle with the uncancelled-magnitude
+floors of the other backward tests. dq is left to those tests: dq = sum_j dS_j k_j, and the
+keys' component RISE (j / N) u makes its u-component a sum of terms ~RISE times larger than
+the result (sum_j dS_j = 0), so its error measures the rounding of dS as an operand (bfloat16:
+2^-9 of that sum; float32: scores of magnitude RISE) rather than the weights; dk and de carry
+the same rebuilt weights without that amplification.
 
 Tolerances. Scores of magnitude RISE carry RISE times the absolute rounding of scores of order
 one, so float32 outputs are held to F32_TOL_RISING = 5e-5 here instead of 1e-5; bfloat16 ones
@@ -147,6 +154,53 @@ def test_rising_logits_gated(case):
         if t == 0:
             assert rel(_host(y), ref_y) <= F32_TOL_RISING
         assert rel(_host(ty)[t], ref_ty) <= F32_TOL_RISING, f"tangent {t}"
+
+
+# The reverse mode rebuilds every weight from the stored lse, P = 2^(s log2 e - lse log2 e):
+# with scores of magnitude RISE the two terms are large and nearly equal for the keys that
+# carry the weight. name, B, N, H, D, n_phys, bias, bf16
+BWD_CASES = [
+    ("bwd_fp32_n64_d32_bias", 4, 64, 2, 32, 50, True, False),
+    ("bwd_fp32_n64_d64", 3, 64, 2, 64, 48, False, False),
+    ("bwd_fp32_n256_d64_bias", 2, 256, 2, 64, 230, True, False),
+    ("bwd_bf16_n64_d64", 4, 64, 2, 64, 48, False, True),
+    ("bwd_bf16_n200_d32_bias", 2, 200, 2, 32, 180, True, True),
+]
+
+
+@pytest.mark.parametrize("case", BWD_CASES, ids=[c[0] for c in BWD_CASES])
+def test_rising_logits_bwd(case):
+    from hamiltonzero_amd import kernels
+    from test_gpu_parity import vjp_floors  # uncancelled magnitudes of dq, dk, de
+
+    name, B, N, H, D, n_phys, with_e, bf16 = case
+    _say(f"rising logits {name}")
+    q, k, v, u, rng = rising(zlib.crc32(name.encode()) % 1000, B, N, N, H, D)
+    mask = np.zeros((B, N), dtype=bool)
+    for b in range(B):
+        mask[b, np.sort(rng.permutation(N)[:n_phys])] = True
+    e = rng.standard_normal((B, N, H, N), dtype=np.float32) * np.float32(0.5) if with_e else None
+    dout = rng.standard_normal((B, N, H, D), dtype=np.float32)
+    a = dict(q=q, k=k, v=v, e=e, dout=dout)
+    if bf16:
+        a = {n: None if x is None else _bf16_round(x) for n, x in a.items()}
+    dt = torch.bfloat16 if bf16 else torch.float32
+    d = {n: _dev(x, dt) for n, x in a.items()}
+    dmask = _dev(mask, None)
+    tol = BF16_TOL if bf16 else F32_TOL_RISING
+    out, lse = kernels.mhsea_fwd(d["q"], d["k"], d["v"], dmask, d["e"])
+    dq, dk, de, dv = kernels.mhsea_bwd(d["q"], d["k"], d["v"], dmask, lse, out, d["dout"], d["e"], want_de=with_e)
+    torch.cuda.synchronize()
+    a["mask"] = mask
+    opts = dict(scale=1.0, key_mask=False, e_layout="qhk")
+    ref = O.vjp(a["q"], a["k"], a["e"], a["v"], mask, a["dout"], **opts)
+    floors = vjp_floors(a, opts)
+    for nm, got, want in zip(("dq", "dk", "de", "dv"), (dq, dk, de, dv), ref):
+        if got is None or nm == "dq":
+            continue
+        g = _host(got).astype(np.float64)
+        bound = max(np.max(np.abs(want)), floors[nm])
+        assert np.max(np.abs(g - want)) <= tol * bound, nm
 
 
 # B, Nq, Nk, H, D, n_phys (None: no mask), gated
